@@ -1,0 +1,67 @@
+"""ChronoQuant attention dispatch (reference attention.py:1-74).
+
+Fused path: one query token per sequence over the compressed cache, run by
+the gfx950 split-K decode kernel (cq_decode_attn).  The reference takes it
+only for B == 1 (its Metal kernel has no batch axis); the gfx950 kernel has
+one, so any batch size with q_len == 1 takes it here.
+
+Fallback (q_len > 1, array masks, use_fused=False): reconstruct fp16 K/V on
+the GPU (cq_reconstruct) and run dense GQA attention with the reference's
+rounding points: q' = fp16(q * fp16(scale)), fp16 scores, mask, softmax in
+fp32 rounded to the query dtype, fp16 weights @ V.
+"""
+from __future__ import annotations
+
+import torch
+
+from .kernels import MAX_FUSED_HEAD_DIM, chronoquant_sdpa_kernel
+
+
+def _apply_mask(scores: torch.Tensor, mask):
+    """attention.py:8-20."""
+    if mask is None:
+        return scores
+    if isinstance(mask, str):
+        q_len, k_len = scores.shape[-2:]
+        q_idx = torch.arange(k_len - q_len, k_len, device=scores.device)
+        k_idx = torch.arange(k_len, device=scores.device)
+        mask = q_idx[:, None] >= k_idx[None]
+    mask = mask.to(scores.device)
+    if mask.dtype == torch.bool:
+        return torch.where(mask, scores, torch.finfo(scores.dtype).min)
+    return scores + mask.to(scores.dtype)
+
+
+def chronoquant_sdpa(queries: torch.Tensor, keys, values, cache, scale: float, mask=None):
+    """ChronoQuant SDPA with fused generation path and reconstruct fallback.
+
+    queries: [B, n_q_heads, q_len, D]; keys/values are the placeholders
+    update_and_fetch returned (attention reads the cache).
+    """
+    batch, n_q_heads, q_len, head_dim = queries.shape
+    use_fused = (
+        cache.use_fused
+        and q_len == 1
+        and cache.offset > 0
+        and head_dim <= MAX_FUSED_HEAD_DIM
+        and (mask is None or (isinstance(mask, str) and mask == "causal"))
+    )
+    if use_fused:
+        q = queries.reshape(batch, n_q_heads, head_dim)
+        out = chronoquant_sdpa_kernel(q, cache, scale)
+        return out.reshape(batch, n_q_heads, q_len, head_dim)
+
+    full_k, full_v = cache.reconstruct_history()
+    n_kv_heads = full_k.shape[1]
+    n_repeats = n_q_heads // n_kv_heads
+    # weak-scalar semantics: scale is rounded to the query dtype first
+    q_scaled = queries * torch.tensor(scale, dtype=queries.dtype, device=queries.device)
+    q_grouped = q_scaled.reshape(batch, n_kv_heads, n_repeats, q_len, head_dim)
+    dt = torch.promote_types(queries.dtype, full_k.dtype)
+    k_t = full_k.to(dt).transpose(-1, -2).contiguous()[:, :, None]
+    v_g = full_v.to(dt)[:, :, None]
+    scores = torch.matmul(q_grouped.to(dt), k_t)
+    scores = _apply_mask(scores, mask)
+    weights = torch.softmax(scores.float(), dim=-1).to(dt)
+    output = torch.matmul(weights, v_g)
+    return output.reshape(batch, n_q_heads, q_len, head_dim).to(queries.dtype)

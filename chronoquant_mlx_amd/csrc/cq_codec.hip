@@ -1,0 +1,431 @@
+// cq_codec.hip — encode side of the ChronoQuant hot path on gfx950:
+// residual quantisation (codec), INT4 packing, the fused append (I-frame or
+// quantise+pack in place) and the fp16 reconstruction used by the fallback
+// attention path.  One wavefront per (token, kv head) row; the row absmax is
+// a DPP reduction; every floating-point op is rounded to the input dtype the
+// way the reference's MLX arrays round it.
+#include <hip/hip_runtime.h>
+#include <math.h>
+
+#include "cq_device.h"
+
+namespace cq {
+
+// Per-lane slice of one row: dims [lane*E, lane*E + E), E in {1, 2, 4}.
+constexpr int kMaxE = 4;
+
+__host__ __device__ inline int dims_per_lane(int D) {
+  return D <= 64 ? 1 : (D <= 128 ? 2 : 4);
+}
+
+// Residual quantisation of one row held by one wavefront.
+// Follows ChronoQuantCodecMLX.quantize_delta (reference codec.py:23-65):
+//   amax = max|d|; s = R(amax/(h-1)); dead zone: thr = R(amax*R(dz)),
+//   d = |d| < thr ? 0 : d, s = R(max(amax',eps-guard)/(h-1));
+//   code = clip(rint(R(d/s_safe)), -h, h-1); code = 0 if s < eps.
+// R rounds to the dtype; eps = R(1e-10) (0 for fp16, so the guards never
+// fire there).  A NaN quotient (0/0 for an all-zero fp16 row) gives code 0.
+template <int DT>
+__device__ __forceinline__ float codec_row(float (&d)[kMaxE], int E, int bits,
+                                           float dz, int (&code)[kMaxE]) {
+  using T = Dt<DT>;
+  const int half = (1 << bits) >> 1;
+  const float hm1 = (float)(half - 1);
+  const float eps = T::round(1e-10f);
+  float a = 0.f;
+#pragma unroll
+  for (int i = 0; i < kMaxE; ++i)
+    if (i < E) a = fmaxf(a, fabsf(d[i]));
+  const float amax = wave_max(a);
+  float scale = T::round(amax / hm1);
+  if (dz > 0.f) {
+    const float thr = T::round(amax * T::round(dz));
+    float a2 = 0.f;
+#pragma unroll
+    for (int i = 0; i < kMaxE; ++i) {
+      if (i < E) {
+        if (fabsf(d[i]) < thr) d[i] = 0.f;
+        a2 = fmaxf(a2, fabsf(d[i]));
+      }
+    }
+    const float amax_c = wave_max(a2);
+    const float amax_safe = (amax_c < eps) ? amax : amax_c;
+    scale = T::round(amax_safe / hm1);
+  }
+  const float scale_safe = (scale < eps) ? 1.0f : scale;
+#pragma unroll
+  for (int i = 0; i < kMaxE; ++i) {
+    const float q = T::round(d[i] / scale_safe);
+    int c;
+    if (q != q) {
+      c = 0;
+    } else {
+      float r = rintf(q);  // round half to even
+      r = fminf(fmaxf(r, (float)(-half)), hm1);
+      c = (int)r;
+    }
+    if (scale < eps) c = 0;
+    code[i] = c;
+  }
+  return scale;
+}
+
+// Pack this lane's E nibbles into its part of word (lane*E)/8 and OR the
+// 8/E lanes of that word together.  nibble = clip(code + 8, 0, 15); dims at
+// or past D carry nibble 0 (reference kernels.py:40-43, MSL :15-21).
+__device__ __forceinline__ uint32_t pack_lane(const int (&code)[kMaxE], int E,
+                                              int lane, int D) {
+  uint32_t part = 0;
+#pragma unroll
+  for (int i = 0; i < kMaxE; ++i) {
+    if (i < E) {
+      const int dim = lane * E + i;
+      int u = code[i] + 8;
+      u = u < 0 ? 0 : (u > 15 ? 15 : u);
+      if (dim < D) part |= (uint32_t)u << (4 * (dim & 7));
+    }
+  }
+  if (E == 1) return group_or<8>(part);
+  if (E == 2) return group_or<4>(part);
+  return group_or<2>(part);
+}
+
+// ---------------------------------------------------------------------------
+// cq_quantize_delta: one wavefront per row
+// ---------------------------------------------------------------------------
+template <int DT>
+__global__ __launch_bounds__(256) void quantize_delta_kernel(
+    const void *__restrict__ delta, int64_t n_rows, int D, int bits, float dz,
+    int8_t *__restrict__ codes, uint16_t *__restrict__ scales) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+  if (row >= n_rows) return;  // wave-uniform
+  const int E = dims_per_lane(D);
+  float d[kMaxE];
+  int code[kMaxE];
+#pragma unroll
+  for (int i = 0; i < kMaxE; ++i) {
+    const int dim = lane * E + i;
+    d[i] = (i < E && dim < D) ? Dt<DT>::load(delta, row * D + dim) : 0.f;
+  }
+  const float s = codec_row<DT>(d, E, bits, dz, code);
+#pragma unroll
+  for (int i = 0; i < kMaxE; ++i) {
+    const int dim = lane * E + i;
+    if (i < E && dim < D) codes[row * D + dim] = (int8_t)code[i];
+  }
+  if (lane == 0) scales[row] = f2h(s);
+}
+
+// ---------------------------------------------------------------------------
+// cq_pack_int4 / cq_unpack_int4: one thread per word
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void pack_kernel(const int8_t *__restrict__ codes,
+                                                   int64_t n_words, int D, int W,
+                                                   uint32_t *__restrict__ packed) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n_words) return;
+  const int64_t row = i / W;
+  const int w = (int)(i - row * W);
+  uint32_t word = 0;
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    const int dim = 8 * w + k;
+    if (dim < D) {
+      int u = (int)codes[row * D + dim] + 8;
+      u = u < 0 ? 0 : (u > 15 ? 15 : u);
+      word |= (uint32_t)u << (4 * k);
+    }
+  }
+  packed[i] = word;
+}
+
+__global__ __launch_bounds__(256) void unpack_kernel(const uint32_t *__restrict__ packed,
+                                                     int64_t n_words, int D, int W,
+                                                     int8_t *__restrict__ codes) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n_words) return;
+  const int64_t row = i / W;
+  const int w = (int)(i - row * W);
+  const uint32_t word = packed[i];
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    const int dim = 8 * w + k;
+    if (dim < D) codes[row * D + dim] = (int8_t)((int)((word >> (4 * k)) & 0xfu) - 8);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// cq_append: one wavefront per (component, b, new token s, kv head)
+// ---------------------------------------------------------------------------
+struct AppendArgs {
+  cq_component comp[2];
+  const void *x[2];
+  int64_t xs[2][3];  // element strides b, h, s
+  int B, H, D, W;
+  int64_t S;
+  const int32_t *offsets;
+  int64_t offset;
+};
+
+template <int DT>
+__global__ __launch_bounds__(256) void append_kernel(AppendArgs a) {
+  const int lane = threadIdx.x & 63;
+  int64_t item = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+  const int64_t per_comp = (int64_t)a.B * a.S * a.H;
+  if (item >= 2 * per_comp) return;  // wave-uniform
+  const int ci = (int)(item / per_comp);
+  item -= ci * per_comp;
+  const int h = (int)(item % a.H);
+  item /= a.H;
+  const int64_t s = item % a.S;
+  const int b = (int)(item / a.S);
+
+  const cq_component &c = a.comp[ci];
+  const int D = a.D, W = a.W, E = dims_per_lane(D);
+  const int64_t off = a.offsets ? (int64_t)a.offsets[b] : a.offset;
+  const int64_t t = off + s;
+  const int stride = c.stride;
+  const int64_t g = t / stride;
+  const int64_t bh = (int64_t)b * a.H + h;
+  const void *x = a.x[ci];
+  const int64_t xrow = b * a.xs[ci][0] + h * a.xs[ci][1] + s * a.xs[ci][2];
+
+  float v[kMaxE];
+#pragma unroll
+  for (int i = 0; i < kMaxE; ++i) {
+    const int dim = lane * E + i;
+    v[i] = (i < E && dim < D) ? Dt<DT>::load(x, xrow + dim) : 0.f;
+  }
+
+  if (t - g * stride == 0) {  // I-frame: fp16(token), reference cache.py:103-105
+    if (g >= c.cap_keyframes) return;
+    uint16_t *row = c.keyframes + (bh * c.cap_keyframes + g) * D;
+#pragma unroll
+    for (int i = 0; i < kMaxE; ++i) {
+      const int dim = lane * E + i;
+      if (i < E && dim < D) row[dim] = f2h(v[i]);
+    }
+    return;
+  }
+
+  const int64_t slot = t - g - 1;
+  if (slot >= c.cap_pframes || g >= c.cap_keyframes) return;
+  // Anchor = fp16 I-frame of group g: from the cache if it predates this
+  // call, else straight from the new tokens (same fp16 value), so the waves
+  // of one launch never depend on each other.
+  const int64_t ta = g * stride;
+  float d[kMaxE];
+  if (ta >= off) {
+    const int64_t arow = b * a.xs[ci][0] + h * a.xs[ci][1] + (ta - off) * a.xs[ci][2];
+#pragma unroll
+    for (int i = 0; i < kMaxE; ++i) {
+      const int dim = lane * E + i;
+      const float an = (i < E && dim < D) ? h2f(f2h(Dt<DT>::load(x, arow + dim))) : 0.f;
+      d[i] = Dt<DT>::round(v[i] - Dt<DT>::round(an));  // cache.py:113
+    }
+  } else {
+    const uint16_t *arow = c.keyframes + (bh * c.cap_keyframes + g) * D;
+#pragma unroll
+    for (int i = 0; i < kMaxE; ++i) {
+      const int dim = lane * E + i;
+      const float an = (i < E && dim < D) ? h2f(arow[dim]) : 0.f;
+      d[i] = Dt<DT>::round(v[i] - Dt<DT>::round(an));
+    }
+  }
+  int code[kMaxE];
+  const float sc = codec_row<DT>(d, E, c.delta_bits, c.dead_zone, code);
+  const uint32_t word = pack_lane(code, E, lane, D);
+  const int wl = lane * E;
+  if ((wl & 7) == 0 && (wl >> 3) < W)
+    c.packed[(bh * c.cap_pframes + slot) * W + (wl >> 3)] = word;
+  if (lane == 0) c.scales[bh * c.cap_pframes + slot] = f2h(sc);
+}
+
+// ---------------------------------------------------------------------------
+// cq_reconstruct: one thread per (b, h, t, word) — reference cache.py:131-156
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void reconstruct_kernel(cq_component c, int B, int H,
+                                                          int D, int W, int64_t T,
+                                                          uint16_t *__restrict__ out) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t total = (int64_t)B * H * T * W;
+  if (i >= total) return;
+  const int w = (int)(i % W);
+  const int64_t bht = i / W;
+  const int64_t t = bht % T;
+  const int64_t bh = bht / T;
+  const int64_t g = t / c.stride;
+  const bool is_p = (t - g * c.stride) != 0;
+  const uint16_t *anc = c.keyframes + (bh * c.cap_keyframes + g) * D;
+  uint16_t *o = out + bht * D;
+  uint32_t word = 0;
+  float s = 0.f;
+  if (is_p) {
+    const int64_t slot = t - g - 1;
+    word = c.packed[(bh * c.cap_pframes + slot) * W + w];
+    s = h2f(c.scales[bh * c.cap_pframes + slot]);
+  }
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    const int dim = 8 * w + k;
+    if (dim >= D) break;
+    float delta = 0.f;
+    if (is_p) delta = h2f(f2h((float)((int)((word >> (4 * k)) & 0xfu) - 8) * s));
+    o[dim] = f2h(h2f(anc[dim]) + delta);  // fp16 add, cache.py:156
+  }
+}
+
+// ---------------------------------------------------------------------------
+// host side
+// ---------------------------------------------------------------------------
+static int launch_status() {
+  return hipGetLastError() == hipSuccess ? CQ_OK : CQ_ERR_LAUNCH;
+}
+
+static bool bits_ok(int bits) { return bits >= 2 && bits <= 4; }
+
+int validate_cache(const cq_cache_desc *c) {
+  if (!c) return CQ_ERR_ARG;
+  if (c->batch < 1 || c->n_kv_heads < 1) return CQ_ERR_SHAPE;
+  if (c->head_dim < 1 || c->head_dim > kMaxHeadDim) return CQ_ERR_SHAPE;
+  for (const cq_component *p : {&c->k, &c->v}) {
+    if (!p->keyframes || !p->packed || !p->scales) return CQ_ERR_ARG;
+    if (p->stride < 1 || !bits_ok(p->delta_bits)) return CQ_ERR_ARG;
+    if (!(p->dead_zone >= 0.f)) return CQ_ERR_ARG;
+    if (p->cap_keyframes < 1 || p->cap_pframes < 1) return CQ_ERR_CAPACITY;
+  }
+  return CQ_OK;
+}
+
+int64_t num_keyframes(int64_t n, int stride) { return n <= 0 ? 0 : (n - 1) / stride + 1; }
+int64_t num_pframes(int64_t n, int stride) { return n - num_keyframes(n, stride); }
+
+}  // namespace cq
+
+using namespace cq;
+
+extern "C" {
+
+const char *cq_status_string(int32_t status) {
+  switch (status) {
+    case CQ_OK: return "ok";
+    case CQ_ERR_ARG: return "invalid argument (null pointer or bad scalar)";
+    case CQ_ERR_SHAPE: return "shape out of range (head_dim must be 1..256, heads/batch >= 1)";
+    case CQ_ERR_DTYPE: return "unsupported dtype";
+    case CQ_ERR_ALIGN: return "pointer misaligned";
+    case CQ_ERR_CAPACITY: return "cache capacity exceeded";
+    case CQ_ERR_WORKSPACE: return "workspace missing or too small";
+    case CQ_ERR_UNSUPPORTED: return "unsupported configuration";
+    case CQ_ERR_LAUNCH: return "kernel launch failed";
+    default: return "unknown status";
+  }
+}
+
+int cq_quantize_delta(const void *delta, int32_t dtype, int64_t n_rows, int32_t head_dim,
+                      int32_t delta_bits, float dead_zone, int8_t *codes,
+                      uint16_t *scales, cq_stream_t stream) {
+  if (n_rows < 0) return CQ_ERR_ARG;
+  if (head_dim < 1 || head_dim > kMaxHeadDim) return CQ_ERR_SHAPE;
+  if (!bits_ok(delta_bits) || !(dead_zone >= 0.f)) return CQ_ERR_ARG;
+  if (n_rows == 0) return CQ_OK;
+  if (!delta || !codes || !scales) return CQ_ERR_ARG;
+  const dim3 grid((unsigned)((n_rows + 3) / 4)), block(256);
+  hipStream_t st = (hipStream_t)stream;
+  switch (dtype) {
+    case CQ_F16: quantize_delta_kernel<CQ_F16><<<grid, block, 0, st>>>(delta, n_rows, head_dim, delta_bits, dead_zone, codes, scales); break;
+    case CQ_BF16: quantize_delta_kernel<CQ_BF16><<<grid, block, 0, st>>>(delta, n_rows, head_dim, delta_bits, dead_zone, codes, scales); break;
+    case CQ_F32: quantize_delta_kernel<CQ_F32><<<grid, block, 0, st>>>(delta, n_rows, head_dim, delta_bits, dead_zone, codes, scales); break;
+    default: return CQ_ERR_DTYPE;
+  }
+  return launch_status();
+}
+
+int cq_pack_int4(const int8_t *codes, int64_t n_rows, int32_t head_dim, uint32_t *packed,
+                 cq_stream_t stream) {
+  if (n_rows < 0 || head_dim < 1) return CQ_ERR_SHAPE;
+  if (n_rows == 0) return CQ_OK;
+  if (!codes || !packed) return CQ_ERR_ARG;
+  const int W = (head_dim + 7) / 8;
+  const int64_t n = n_rows * W;
+  pack_kernel<<<dim3((unsigned)((n + 255) / 256)), dim3(256), 0, (hipStream_t)stream>>>(
+      codes, n, head_dim, W, packed);
+  return launch_status();
+}
+
+int cq_unpack_int4(const uint32_t *packed, int64_t n_rows, int32_t head_dim, int8_t *codes,
+                   cq_stream_t stream) {
+  if (n_rows < 0 || head_dim < 1) return CQ_ERR_SHAPE;
+  if (n_rows == 0) return CQ_OK;
+  if (!codes || !packed) return CQ_ERR_ARG;
+  const int W = (head_dim + 7) / 8;
+  const int64_t n = n_rows * W;
+  unpack_kernel<<<dim3((unsigned)((n + 255) / 256)), dim3(256), 0, (hipStream_t)stream>>>(
+      packed, n, head_dim, W, codes);
+  return launch_status();
+}
+
+int cq_append(const cq_cache_desc *cache, const void *keys, const int64_t *key_strides,
+              const void *values, const int64_t *value_strides, int32_t dtype,
+              int64_t n_new, const int32_t *offsets, int64_t offset, cq_stream_t stream) {
+  int st = validate_cache(cache);
+  if (st) return st;
+  if (n_new < 0 || offset < 0) return CQ_ERR_ARG;
+  if (n_new == 0) return CQ_OK;
+  if (!keys || !values || !key_strides || !value_strides) return CQ_ERR_ARG;
+  if (!offsets) {  // host-side capacity check when positions are known here
+    for (const cq_component *p : {&cache->k, &cache->v}) {
+      if (num_keyframes(offset + n_new, p->stride) > p->cap_keyframes ||
+          num_pframes(offset + n_new, p->stride) > p->cap_pframes)
+        return CQ_ERR_CAPACITY;
+    }
+  }
+  AppendArgs a;
+  a.comp[0] = cache->k;
+  a.comp[1] = cache->v;
+  a.x[0] = keys;
+  a.x[1] = values;
+  for (int i = 0; i < 3; ++i) {
+    a.xs[0][i] = key_strides[i];
+    a.xs[1][i] = value_strides[i];
+  }
+  a.B = cache->batch;
+  a.H = cache->n_kv_heads;
+  a.D = cache->head_dim;
+  a.W = (cache->head_dim + 7) / 8;
+  a.S = n_new;
+  a.offsets = offsets;
+  a.offset = offset;
+  const int64_t items = 2 * (int64_t)a.B * a.S * a.H;
+  const dim3 grid((unsigned)((items + 3) / 4)), block(256);
+  hipStream_t s = (hipStream_t)stream;
+  switch (dtype) {
+    case CQ_F16: append_kernel<CQ_F16><<<grid, block, 0, s>>>(a); break;
+    case CQ_BF16: append_kernel<CQ_BF16><<<grid, block, 0, s>>>(a); break;
+    case CQ_F32: append_kernel<CQ_F32><<<grid, block, 0, s>>>(a); break;
+    default: return CQ_ERR_DTYPE;
+  }
+  return launch_status();
+}
+
+int cq_reconstruct(const cq_cache_desc *cache, int32_t component, int64_t seq_len,
+                   uint16_t *out, cq_stream_t stream) {
+  int st = validate_cache(cache);
+  if (st) return st;
+  if (component != CQ_KEYS && component != CQ_VALUES) return CQ_ERR_ARG;
+  if (seq_len < 0) return CQ_ERR_ARG;
+  if (seq_len == 0) return CQ_OK;
+  if (!out) return CQ_ERR_ARG;
+  const cq_component &c = component == CQ_KEYS ? cache->k : cache->v;
+  if (num_keyframes(seq_len, c.stride) > c.cap_keyframes ||
+      num_pframes(seq_len, c.stride) > c.cap_pframes)
+    return CQ_ERR_CAPACITY;
+  const int D = cache->head_dim, W = (D + 7) / 8;
+  const int64_t total = (int64_t)cache->batch * cache->n_kv_heads * seq_len * W;
+  reconstruct_kernel<<<dim3((unsigned)((total + 255) / 256)), dim3(256), 0,
+                       (hipStream_t)stream>>>(c, cache->batch, cache->n_kv_heads, D, W,
+                                              seq_len, out);
+  return launch_status();
+}
+
+}  // extern "C"

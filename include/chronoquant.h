@@ -1,0 +1,171 @@
+/*
+ * chronoquant.h — C ABI of the MI355X (gfx950) ChronoQuant KV-cache hot path.
+ *
+ * The library is libchronoquant.so (built from chronoquant_mlx_amd/csrc/*.hip).
+ * Every entry point:
+ *   - returns an int status (CQ_OK == 0); no exception ever crosses the ABI;
+ *   - takes caller-owned DEVICE pointers (the library never allocates device
+ *     memory; scratch space is an explicit workspace argument);
+ *   - is stream ordered and asynchronous (work is enqueued on `stream`, a
+ *     hipStream_t passed as void*; NULL means the legacy default stream);
+ *   - is re-entrant for distinct buffers and streams (no global mutable state).
+ *
+ * Storage layout (identical to the reference's logical tensors; an outer
+ * capacity dimension per (sequence, kv head) lets appends write in place):
+ *   keyframes  fp16   [B][H][cap_keyframes][D]     I-frames (anchors)
+ *   packed     uint32 [B][H][cap_pframes][W]       W = ceil(D/8); nibble i of word w
+ *                                                  holds code(dim 8w+i) + 8, bits 4i..4i+3
+ *   scales     fp16   [B][H][cap_pframes]          one scale per P-frame row
+ * Token t of a sequence is an I-frame iff t % stride == 0; otherwise it is
+ * P-frame slot t - t/stride - 1 coded against anchor t/stride.
+ * The active prefix of each array is exactly the reference's tensor
+ * (cache.py:46-51, cache.py:63-85).
+ */
+#ifndef CHRONOQUANT_H
+#define CHRONOQUANT_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef void *cq_stream_t; /* hipStream_t */
+
+enum cq_status {
+  CQ_OK = 0,
+  CQ_ERR_ARG = 1,         /* null pointer or invalid scalar argument */
+  CQ_ERR_SHAPE = 2,       /* head_dim / heads / lengths out of range */
+  CQ_ERR_DTYPE = 3,       /* unsupported dtype code */
+  CQ_ERR_ALIGN = 4,       /* pointer misaligned for the required vector width */
+  CQ_ERR_CAPACITY = 5,    /* append or read beyond the cache capacity */
+  CQ_ERR_WORKSPACE = 6,   /* workspace missing or smaller than required */
+  CQ_ERR_UNSUPPORTED = 7, /* valid request the library does not implement */
+  CQ_ERR_LAUNCH = 8       /* kernel launch reported an error */
+};
+
+enum cq_dtype { CQ_F16 = 0, CQ_BF16 = 1, CQ_F32 = 2 };
+
+enum cq_component_id { CQ_KEYS = 0, CQ_VALUES = 1 };
+
+/* One compressed component (keys or values) of a batch of sequences. */
+typedef struct cq_component {
+  uint16_t *keyframes;   /* fp16 [B][H][cap_keyframes][D] */
+  uint32_t *packed;      /* [B][H][cap_pframes][W] */
+  uint16_t *scales;      /* fp16 [B][H][cap_pframes] */
+  int64_t cap_keyframes; /* rows reserved per (b, h) */
+  int64_t cap_pframes;   /* rows reserved per (b, h) */
+  int32_t stride;        /* I-frame period, >= 1 */
+  int32_t delta_bits;    /* residual bits, 2..4 (codes live in INT4 lanes) */
+  float dead_zone;       /* dead-zone ratio, >= 0 */
+  int32_t reserved;
+} cq_component;
+
+typedef struct cq_cache_desc {
+  int32_t batch;      /* B */
+  int32_t n_kv_heads; /* H */
+  int32_t head_dim;   /* D, 1..256 */
+  int32_t reserved;
+  cq_component k;
+  cq_component v;
+} cq_cache_desc;
+
+/* Residual quantisation of n_rows rows of head_dim values each.
+ * Replaces ChronoQuantCodecMLX.quantize_delta (reference codec.py:23-65):
+ * per row scale = absmax/(2^bits/2 - 1) with the dead-zone rescale, codes =
+ * clip(round_half_even(delta/scale), -2^bits/2, 2^bits/2 - 1), computed with
+ * the rounding of `dtype` after every operation; scales returned as fp16.
+ * delta: [n_rows][head_dim] of `dtype`; codes: int8 [n_rows][head_dim];
+ * scales: fp16 [n_rows]. */
+int cq_quantize_delta(const void *delta, int32_t dtype, int64_t n_rows,
+                      int32_t head_dim, int32_t delta_bits, float dead_zone,
+                      int8_t *codes, uint16_t *scales, cq_stream_t stream);
+
+/* INT4 packing. Replaces pack_int4_codes (reference kernels.py:34-54, MSL
+ * kernels.py:9-22): nibble = clip(code + 8, 0, 15), 8 nibbles per uint32,
+ * head_dim padded to a multiple of 8 with nibble 0.
+ * codes: int8 [n_rows][head_dim]; packed: [n_rows][ceil(head_dim/8)]. */
+int cq_pack_int4(const int8_t *codes, int64_t n_rows, int32_t head_dim,
+                 uint32_t *packed, cq_stream_t stream);
+
+/* Inverse of cq_pack_int4. Replaces unpack_int4_codes (reference
+ * kernels.py:57-61): code = ((word >> 4i) & 15) - 8, truncated to head_dim. */
+int cq_unpack_int4(const uint32_t *packed, int64_t n_rows, int32_t head_dim,
+                   int8_t *codes, cq_stream_t stream);
+
+/* Append n_new tokens per sequence to both components: I-frame every stride,
+ * otherwise residual against the anchor, quantised and packed in place.
+ * Replaces ChronoQuantCache._append_component / update_and_fetch (reference
+ * cache.py:87-129, 198-215) fused with the codec and the pack kernel.
+ * keys / values: element (b, h, s, d) at base + b*sb + h*sh + s*ss + d
+ *   (strides in elements, [3] = {sb, sh, ss}; d is contiguous), of `dtype`.
+ * Positions: token s of sequence b lands at position offsets[b] + s when
+ *   `offsets` (device int32 [B]) is non-NULL, else at `offset` + s.
+ * The caller guarantees the capacities hold the new rows. */
+int cq_append(const cq_cache_desc *cache, const void *keys,
+              const int64_t *key_strides, const void *values,
+              const int64_t *value_strides, int32_t dtype, int64_t n_new,
+              const int32_t *offsets, int64_t offset, cq_stream_t stream);
+
+/* Full fp16 reconstruction of one component for positions [0, seq_len).
+ * Replaces ChronoQuantCache._reconstruct_component (reference
+ * cache.py:131-156): r = fp16(anchor + fp16(fp16(code) * scale)) for
+ * P-frames, the anchor for I-frames.  out: fp16 [B][H][seq_len][D]. */
+int cq_reconstruct(const cq_cache_desc *cache, int32_t component,
+                   int64_t seq_len, uint16_t *out, cq_stream_t stream);
+
+/* Bytes of workspace cq_decode_attn needs for this shape.  The workspace
+ * must be zero-filled once before its first use; every call leaves its
+ * counters at zero again, so it can be reused without clearing.  Calls that
+ * share one workspace must be ordered on one stream. */
+size_t cq_decode_workspace_size(int32_t batch, int32_t n_kv_heads,
+                                int32_t n_q_heads, int32_t head_dim,
+                                int64_t max_seq_len);
+
+/* Fused dequant + GQA scaled-dot-product attention for one query token per
+ * sequence over the compressed cache (split-K flash decode; the last
+ * workgroup of each kv head merges the splits).  Replaces
+ * chronoquant_sdpa_kernel (reference kernels.py:248-279, MSL :79-228) and the
+ * fused branch of chronoquant_sdpa (attention.py:45-59), generalised to B>=1
+ * and per-sequence lengths.
+ * q: [B][n_q_heads][head_dim] of q_dtype; q' = q*scale is rounded to q_dtype
+ *   as in attention.py:46.  q head j reads kv head j / (n_q_heads/H).
+ * Lengths: seq_lens (device int32 [B]) when non-NULL, else seq_len for all.
+ * out: [B][n_q_heads][head_dim] of out_dtype. */
+int cq_decode_attn(const cq_cache_desc *cache, const void *q, int32_t q_dtype,
+                   int32_t n_q_heads, float scale, const int32_t *seq_lens,
+                   int64_t seq_len, int64_t max_seq_len, void *out,
+                   int32_t out_dtype, void *workspace, size_t workspace_bytes,
+                   cq_stream_t stream);
+
+/* Same contract as cq_decode_attn but always runs the portable (VALU) decode
+ * kernel, for any head_dim <= 256 and q dtype; the test suite uses it to
+ * check the specialised kernels against a second GPU implementation. */
+int cq_decode_attn_generic(const cq_cache_desc *cache, const void *q,
+                           int32_t q_dtype, int32_t n_q_heads, float scale,
+                           const int32_t *seq_lens, int64_t seq_len,
+                           int64_t max_seq_len, void *out, int32_t out_dtype,
+                           void *workspace, size_t workspace_bytes,
+                           cq_stream_t stream);
+
+/* Uncompressed fp16 split-K flash decode, the comparison baseline the
+ * compressed path has to beat (no reference counterpart: it stands for the
+ * host framework's own fp16 SDPA over a plain KVCache).
+ * k, v: fp16 [B][H][cap_tokens][D]; same q / out / workspace contract. */
+int cq_fp16_decode_attn(const uint16_t *k, const uint16_t *v,
+                        int64_t cap_tokens, int32_t batch, int32_t n_kv_heads,
+                        int32_t head_dim, const void *q, int32_t q_dtype,
+                        int32_t n_q_heads, float scale, const int32_t *seq_lens,
+                        int64_t seq_len, int64_t max_seq_len, void *out,
+                        int32_t out_dtype, void *workspace,
+                        size_t workspace_bytes, cq_stream_t stream);
+
+/* Static description of a status code. */
+const char *cq_status_string(int32_t status);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* CHRONOQUANT_H */

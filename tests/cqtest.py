@@ -1,0 +1,67 @@
+"""Shared helpers of the GPU parity tests: build the same cache on the GPU
+(through libchronoquant.so) and in the CPU oracle, and compare."""
+from __future__ import annotations
+
+import numpy as np
+import torch
+
+from oracle import oracle as O
+
+ATOL, RTOL = 2e-3, 1e-2  # decode parity bar
+
+
+def to_gpu(x: np.ndarray, dtype=torch.float16) -> torch.Tensor:
+    return torch.from_numpy(np.ascontiguousarray(x)).to("cuda").to(dtype)
+
+
+def build_gpu_cache(k: np.ndarray, v: np.ndarray, *, stride_k, stride_v, bits_k=4, bits_v=4,
+                    dz_k=0.0, dz_v=0.0, chunks=None, dtype=torch.float16):
+    """ChronoQuantCache filled with fp16 k, v [B, H, T, D] (appended in chunks)."""
+    from chronoquant_mlx_amd import ChronoQuantCache
+    cache = ChronoQuantCache(stride_k=stride_k, stride_v=stride_v, delta_bits_k=bits_k,
+                             delta_bits_v=bits_v, dead_zone_k=dz_k, dead_zone_v=dz_v)
+    T = k.shape[2]
+    kt, vt = to_gpu(k, dtype), to_gpu(v, dtype)
+    if chunks is None:
+        chunks = [T]
+    pos = 0
+    for S in chunks:
+        cache.update_and_fetch(kt[:, :, pos: pos + S], vt[:, :, pos: pos + S])
+        pos += S
+    assert pos == T
+    return cache
+
+
+def build_oracle(k_b: np.ndarray, v_b: np.ndarray, *, stride_k, stride_v, bits_k=4, bits_v=4,
+                 dz_k=0.0, dz_v=0.0, dtype="f16"):
+    """Oracle components of ONE sequence (k_b, v_b [H, T, D])."""
+    H, T, D = k_b.shape
+    ck = O.OracleComponent(H, D, stride_k, bits_k, dz_k, capacity=T)
+    cv = O.OracleComponent(H, D, stride_v, bits_v, dz_v, capacity=T)
+    ck.append(k_b, dtype)
+    cv.append(v_b, dtype)
+    return ck, cv
+
+
+def assert_state_equal(cache, b: int, ck, cv):
+    """GPU cache state of sequence b == oracle state, bit for bit."""
+    st = cache.state
+    for i, comp in ((0, ck), (1, cv)):
+        kf, pk, sc = comp.active()
+        g_kf = st[i][b].cpu().numpy()
+        g_pk = st[2 + 2 * i][b].cpu().numpy()
+        g_sc = st[3 + 2 * i][b].cpu().numpy()
+        assert np.array_equal(g_kf.view(np.uint16), kf.view(np.uint16)), f"keyframes[{i}] differ"
+        diff = np.argwhere(g_pk != pk)
+        assert diff.size == 0, f"packed[{i}] differ at {diff[:5].tolist()} ({len(diff)} words)"
+        assert np.array_equal(g_sc.view(np.uint16), sc.view(np.uint16)), f"scales[{i}] differ"
+
+
+def assert_close(got, ref, atol=ATOL, rtol=RTOL, what=""):
+    got = np.asarray(got, np.float64)
+    ref = np.asarray(ref, np.float64)
+    err = np.abs(got - ref)
+    rel = np.linalg.norm(got - ref) / max(np.linalg.norm(ref), 1e-30)
+    assert err.max() <= atol, f"{what} max-abs {err.max():.3e} > {atol}"
+    assert rel <= rtol, f"{what} rel {rel:.3e} > {rtol}"
+    return float(err.max()), float(rel)

@@ -1,0 +1,181 @@
+"""GPU parity of the fused decode attention against the oracle's restatement of
+the reference's reconstruct-fallback path (attention.py:61-74).
+
+Bar (from the BASELINE north star): max-abs <= 2e-3 and relative L2 <= 1e-2
+against the fallback output on identical seeded inputs.
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as O
+from tests.cqtest import assert_close, build_gpu_cache, build_oracle, to_gpu
+
+pytestmark = pytest.mark.gpu
+
+
+def decode_gpu(cache, q_np, scale, generic=False, seq_lens=None):
+    from chronoquant_mlx_amd.kernels import chronoquant_sdpa_kernel
+    q = to_gpu(q_np)
+    lens = None if seq_lens is None else torch.tensor(seq_lens, dtype=torch.int32, device="cuda")
+    return chronoquant_sdpa_kernel(q, cache, scale, seq_lens=lens, generic=generic).float().cpu().numpy()
+
+
+def oracle_fallback(ck, cv, q_b, scale):
+    return O.sdpa_fallback(q_b[:, None], ck.reconstruct(), cv.reconstruct(), scale)[:, 0]
+
+
+def run_config(name, T=None, B=None, generic=False, seqs=None):
+    from chronoquant_mlx_amd import synth
+    cfg = synth.CONFIGS[name]
+    B = cfg.B if B is None else B
+    k, v = synth.make_kv(cfg, T=T, B=B)
+    q = synth.make_q(cfg, B=B)
+    params = dict(stride_k=cfg.stride_k, stride_v=cfg.stride_v, bits_k=cfg.delta_bits_k,
+                  bits_v=cfg.delta_bits_v, dz_k=cfg.dead_zone_k, dz_v=cfg.dead_zone_v)
+    cache = build_gpu_cache(k, v, **params)
+    scale = cfg.head_dim ** -0.5
+    out = decode_gpu(cache, q, scale, generic=generic)
+    for b in (range(B) if seqs is None else seqs):
+        ck, cv = build_oracle(k[b], v[b], **params)
+        ref = oracle_fallback(ck, cv, q[b], scale)
+        assert_close(out[b], ref, what=f"{name} b={b}")
+
+
+@pytest.mark.parametrize("generic", [False, True])
+def test_c0_full(generic):
+    run_config("c0", generic=generic)
+
+
+@pytest.mark.parametrize("generic", [False, True])
+def test_c1_full(generic):
+    run_config("c1", generic=generic)
+
+
+def test_c2_two_sequences():
+    # Full-Throttle V3, T = 32768: two of the eight sequences
+    run_config("c2", B=2)
+
+
+@pytest.mark.parametrize("T", [1, 2, 31, 32, 33, 63, 64, 65, 129, 1000])
+def test_short_contexts(T):
+    run_config("c1", T=T)
+
+
+@pytest.mark.parametrize("G,H,D", [(1, 4, 128), (2, 4, 128), (4, 2, 64), (8, 1, 128),
+                                   (4, 2, 72), (3, 2, 256), (16, 1, 128)])
+def test_shapes(G, H, D):
+    rng = np.random.default_rng(G * 100 + D)
+    B, T = 2, 700
+    k = np.cumsum(rng.standard_normal((B, H, T, D)) * 0.1, axis=2).astype(np.float16)
+    v = np.cumsum(rng.standard_normal((B, H, T, D)) * 0.1, axis=2).astype(np.float16)
+    q = rng.standard_normal((B, G * H, D)).astype(np.float16)
+    params = dict(stride_k=16, stride_v=4)
+    cache = build_gpu_cache(k, v, **params)
+    scale = D ** -0.5
+    for generic in (False, True):
+        out = decode_gpu(cache, q, scale, generic=generic)
+        for b in range(B):
+            ck, cv = build_oracle(k[b], v[b], **params)
+            assert_close(out[b], oracle_fallback(ck, cv, q[b], scale), what=f"generic={generic}")
+
+
+def test_ragged_lengths():
+    # per-sequence lengths: sequence b reads only its first L_b tokens and
+    # must equal an independent cache of length L_b
+    rng = np.random.default_rng(21)
+    B, H, T, D, G = 4, 8, 2000, 128, 4
+    k = np.cumsum(rng.standard_normal((B, H, T, D)) * 0.1, axis=2).astype(np.float16)
+    v = np.cumsum(rng.standard_normal((B, H, T, D)) * 0.1, axis=2).astype(np.float16)
+    q = rng.standard_normal((B, G * H, D)).astype(np.float16)
+    params = dict(stride_k=32, stride_v=8)
+    cache = build_gpu_cache(k, v, **params)
+    lens = [2000, 1, 1057, 640]
+    scale = D ** -0.5
+    out = decode_gpu(cache, q, scale, seq_lens=lens)
+    for b, L in enumerate(lens):
+        ck, cv = build_oracle(k[b, :, :L], v[b, :, :L], **params)
+        assert_close(out[b], oracle_fallback(ck, cv, q[b], scale), what=f"b={b} L={L}")
+
+
+def test_scale_and_dtypes():
+    # bf16 queries/output; the scaled query is rounded to the query dtype
+    rng = np.random.default_rng(5)
+    B, H, T, D = 1, 2, 300, 128
+    k = np.cumsum(rng.standard_normal((B, H, T, D)) * 0.1, axis=2).astype(np.float16)
+    v = np.cumsum(rng.standard_normal((B, H, T, D)) * 0.1, axis=2).astype(np.float16)
+    q = rng.standard_normal((B, 4 * H, D)).astype(np.float16)
+    params = dict(stride_k=32, stride_v=8)
+    cache = build_gpu_cache(k, v, **params)
+    from chronoquant_mlx_amd.kernels import chronoquant_sdpa_kernel
+    out32 = chronoquant_sdpa_kernel(to_gpu(q, torch.float32), cache, 0.3,
+                                    out_dtype=torch.float32).cpu().numpy()
+    out16 = decode_gpu(cache, q, 0.3)
+    ck, cv = build_oracle(k[0], v[0], **params)
+    fused = O.sdpa_fused(q[0], ck, cv, 0.3)
+    assert_close(out16[0], fused)
+    assert_close(out32[0], fused)
+
+
+def test_fp16_baseline_matches_exact():
+    from chronoquant_mlx_amd import _lib
+    rng = np.random.default_rng(8)
+    B, H, T, D, G = 2, 8, 3000, 128, 4
+    k = rng.standard_normal((B, H, T, D)).astype(np.float16)
+    v = rng.standard_normal((B, H, T, D)).astype(np.float16)
+    q = rng.standard_normal((B, G * H, D)).astype(np.float16)
+    kt, vt, qt = to_gpu(k), to_gpu(v), to_gpu(q)
+    out = torch.empty(B, G * H, D, dtype=torch.float16, device="cuda")
+    need = _lib.load().cq_decode_workspace_size(B, H, G * H, D, T)
+    ws = torch.zeros(need, dtype=torch.uint8, device="cuda")
+    _lib.call("cq_fp16_decode_attn", kt.data_ptr(), vt.data_ptr(), T, B, H, D, qt.data_ptr(),
+              _lib.CQ_F16, G * H, float(D ** -0.5), None, T, T, out.data_ptr(), _lib.CQ_F16,
+              ws.data_ptr(), need, _lib.stream_of(qt))
+    got = out.float().cpu().numpy()
+    for b in range(B):
+        ref = O.sdpa_exact(q[b], k[b], v[b], D ** -0.5)
+        assert_close(got[b], ref, what=f"fp16 baseline b={b}")
+
+
+def test_sdpa_dispatch_and_fallback():
+    # q_len > 1 takes the reconstruct fallback with the "causal" mask
+    from chronoquant_mlx_amd import chronoquant_sdpa
+    rng = np.random.default_rng(6)
+    B, H, T, D, G, Tq = 1, 2, 200, 64, 2, 7
+    k = np.cumsum(rng.standard_normal((B, H, T, D)) * 0.1, axis=2).astype(np.float16)
+    v = np.cumsum(rng.standard_normal((B, H, T, D)) * 0.1, axis=2).astype(np.float16)
+    q = rng.standard_normal((B, G * H, Tq, D)).astype(np.float16)
+    params = dict(stride_k=8, stride_v=4)
+    cache = build_gpu_cache(k, v, **params)
+    out = chronoquant_sdpa(to_gpu(q), None, None, cache, D ** -0.5, mask="causal")
+    ck, cv = build_oracle(k[0], v[0], **params)
+    ref = O.sdpa_fallback(q[0], ck.reconstruct(), cv.reconstruct(), D ** -0.5, causal=True)
+    assert_close(out[0].float().cpu().numpy(), ref.astype(np.float32))
+    # single query: fused path == fallback path within the bar
+    out1 = chronoquant_sdpa(to_gpu(q[:, :, -1:]), None, None, cache, D ** -0.5)
+    cache.use_fused = False
+    out2 = chronoquant_sdpa(to_gpu(q[:, :, -1:]), None, None, cache, D ** -0.5)
+    assert_close(out1.float().cpu().numpy(), out2.float().cpu().numpy())
+
+
+def test_patch_routes_chronoquant_caches():
+    import chronoquant_mlx_amd as cq
+    from chronoquant_mlx_amd import host
+    rng = np.random.default_rng(3)
+    k = to_gpu(rng.standard_normal((1, 2, 40, 64)).astype(np.float16))
+    q = to_gpu(rng.standard_normal((1, 4, 1, 64)).astype(np.float16))
+    plain = host.KVCache()
+    kk, vv = plain.update_and_fetch(k, k)
+    ref = host.scaled_dot_product_attention(q, kk, vv, plain, 0.125, None)
+    cq.apply()
+    try:
+        c = cq.ChronoQuantCache(stride_k=1, stride_v=1)
+        c.update_and_fetch(k, k)
+        got = host.scaled_dot_product_attention(q, k, k, c, 0.125, None)
+        # stride 1: every token is an exact fp16 I-frame -> same attention
+        assert_close(got.float().cpu().numpy(), ref.float().cpu().numpy())
+        again = host.scaled_dot_product_attention(q, kk, vv, plain, 0.125, None)
+        assert torch.equal(again, ref)
+    finally:
+        cq.revert()
+    assert host.scaled_dot_product_attention is not None
