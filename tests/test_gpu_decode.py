@@ -1,15 +1,18 @@
 """GPU parity of the fused decode attention against the oracle's restatement of
 the reference's reconstruct-fallback path (attention.py:61-74).
 
-Bar (from the BASELINE north star): max-abs <= 2e-3 and relative L2 <= 1e-2
-against the fallback output on identical seeded inputs.
+Bar (from the BASELINE north star): |got - ref| <= 2e-3 + 1e-2*|ref| elementwise
+(and relative L2 <= 1e-2) against the fallback output on identical seeded
+inputs; plus a tight bar (2e-4 + 1e-3*|ref|) against the oracle's restatement of
+the reference's fused-kernel semantics (kernels.py:79-228), which is what the
+gfx950 kernels compute.
 """
 import numpy as np
 import pytest
 import torch
 
 from oracle import oracle as O
-from tests.cqtest import assert_close, build_gpu_cache, build_oracle, to_gpu
+from tests.cqtest import assert_close, assert_tight, build_gpu_cache, build_oracle, to_gpu
 
 pytestmark = pytest.mark.gpu
 
@@ -40,6 +43,7 @@ def run_config(name, T=None, B=None, generic=False, seqs=None):
         ck, cv = build_oracle(k[b], v[b], **params)
         ref = oracle_fallback(ck, cv, q[b], scale)
         assert_close(out[b], ref, what=f"{name} b={b}")
+        assert_tight(out[b], O.sdpa_fused(q[b], ck, cv, scale), what=f"{name} b={b}")
 
 
 @pytest.mark.parametrize("generic", [False, True])
@@ -78,6 +82,27 @@ def test_shapes(G, H, D):
         for b in range(B):
             ck, cv = build_oracle(k[b], v[b], **params)
             assert_close(out[b], oracle_fallback(ck, cv, q[b], scale), what=f"generic={generic}")
+            assert_tight(out[b], O.sdpa_fused(q[b], ck, cv, scale), what=f"generic={generic}")
+
+
+def test_workspace_shared_across_shapes():
+    # regression: calls with different split counts share the per-device
+    # workspace; counters must stay valid between them
+    rng = np.random.default_rng(31)
+    H, D, G = 8, 128, 4
+    params = dict(stride_k=32, stride_v=8)
+    runs = []
+    for B, T in ((1, 5000), (2, 65), (1, 16384), (3, 700), (1, 65), (2, 129)):
+        k = np.cumsum(rng.standard_normal((B, H, T, D)) * 0.1, axis=2).astype(np.float16)
+        v = np.cumsum(rng.standard_normal((B, H, T, D)) * 0.1, axis=2).astype(np.float16)
+        q = rng.standard_normal((B, G * H, D)).astype(np.float16)
+        runs.append((build_gpu_cache(k, v, **params), k, v, q))
+    for _ in range(2):
+        for cache, k, v, q in runs:
+            out = decode_gpu(cache, q, D ** -0.5)
+            for b in range(k.shape[0]):
+                ck, cv = build_oracle(k[b], v[b], **params)
+                assert_tight(out[b], O.sdpa_fused(q[b], ck, cv, D ** -0.5), what=f"T={k.shape[2]}")
 
 
 def test_ragged_lengths():
@@ -96,10 +121,11 @@ def test_ragged_lengths():
     for b, L in enumerate(lens):
         ck, cv = build_oracle(k[b, :, :L], v[b, :, :L], **params)
         assert_close(out[b], oracle_fallback(ck, cv, q[b], scale), what=f"b={b} L={L}")
+        assert_tight(out[b], O.sdpa_fused(q[b], ck, cv, scale), what=f"b={b} L={L}")
 
 
-def test_scale_and_dtypes():
-    # bf16 queries/output; the scaled query is rounded to the query dtype
+def test_output_dtypes_and_fp32_queries():
+    from chronoquant_mlx_amd.kernels import chronoquant_sdpa_kernel
     rng = np.random.default_rng(5)
     B, H, T, D = 1, 2, 300, 128
     k = np.cumsum(rng.standard_normal((B, H, T, D)) * 0.1, axis=2).astype(np.float16)
@@ -107,14 +133,18 @@ def test_scale_and_dtypes():
     q = rng.standard_normal((B, 4 * H, D)).astype(np.float16)
     params = dict(stride_k=32, stride_v=8)
     cache = build_gpu_cache(k, v, **params)
-    from chronoquant_mlx_amd.kernels import chronoquant_sdpa_kernel
-    out32 = chronoquant_sdpa_kernel(to_gpu(q, torch.float32), cache, 0.3,
-                                    out_dtype=torch.float32).cpu().numpy()
-    out16 = decode_gpu(cache, q, 0.3)
     ck, cv = build_oracle(k[0], v[0], **params)
     fused = O.sdpa_fused(q[0], ck, cv, 0.3)
-    assert_close(out16[0], fused)
-    assert_close(out32[0], fused)
+    out16 = decode_gpu(cache, q, 0.3)
+    assert_tight(out16[0], fused)
+    # fp32 output: only fp32 accumulation error remains
+    out32 = chronoquant_sdpa_kernel(to_gpu(q), cache, 0.3, out_dtype=torch.float32)
+    assert_close(out32[0].cpu().numpy(), fused, 2e-5, 1e-5)
+    # fp32 queries: q*scale is not rounded to fp16; compare with binary64
+    # attention on the reconstruction
+    outq = chronoquant_sdpa_kernel(to_gpu(q, torch.float32), cache, 0.3).cpu().numpy()
+    exact = O.sdpa_exact(q[0], ck.reconstruct(), cv.reconstruct(), 0.3)
+    assert_close(outq[0], exact)
 
 
 def test_fp16_baseline_matches_exact():
