@@ -3,9 +3,10 @@ the reference's reconstruct-fallback path (attention.py:61-74).
 
 Bar (from the BASELINE north star): |got - ref| <= 2e-3 + 1e-2*|ref| elementwise
 (and relative L2 <= 1e-2) against the fallback output on identical seeded
-inputs; plus a tight bar (2e-4 + 1e-3*|ref|) against the oracle's restatement of
-the reference's fused-kernel semantics (kernels.py:79-228), which is what the
-gfx950 kernels compute.
+inputs; plus a tight bar against the oracle's restatement of the reference's
+fused-kernel semantics (kernels.py:79-228), which is what the gfx950 kernels
+compute: 2e-4 + 1e-3*|ref| for the portable kernel, 5e-4 + 2e-3*|ref| for the
+MFMA kernel, whose P.V operands hold the softmax weights in fp16.
 """
 import numpy as np
 import pytest
@@ -43,7 +44,8 @@ def run_config(name, T=None, B=None, generic=False, seqs=None):
         ck, cv = build_oracle(k[b], v[b], **params)
         ref = oracle_fallback(ck, cv, q[b], scale)
         assert_close(out[b], ref, what=f"{name} b={b}")
-        assert_tight(out[b], O.sdpa_fused(q[b], ck, cv, scale), what=f"{name} b={b}")
+        assert_tight(out[b], O.sdpa_fused(q[b], ck, cv, scale), what=f"{name} b={b}",
+                     mfma=not generic)
 
 
 @pytest.mark.parametrize("generic", [False, True])
@@ -82,7 +84,8 @@ def test_shapes(G, H, D):
         for b in range(B):
             ck, cv = build_oracle(k[b], v[b], **params)
             assert_close(out[b], oracle_fallback(ck, cv, q[b], scale), what=f"generic={generic}")
-            assert_tight(out[b], O.sdpa_fused(q[b], ck, cv, scale), what=f"generic={generic}")
+            assert_tight(out[b], O.sdpa_fused(q[b], ck, cv, scale), what=f"generic={generic}",
+                         mfma=not generic)
 
 
 def test_workspace_shared_across_shapes():
@@ -137,9 +140,13 @@ def test_output_dtypes_and_fp32_queries():
     fused = O.sdpa_fused(q[0], ck, cv, 0.3)
     out16 = decode_gpu(cache, q, 0.3)
     assert_tight(out16[0], fused)
-    # fp32 output: only fp32 accumulation error remains
+    # fp32 output: no output rounding; what remains is the fp16 rounding of the
+    # softmax weights fed to the MFMA P.V (<= 2^-12 relative per weight, the
+    # rounding point the reference fallback also has) and fp32 accumulation
     out32 = chronoquant_sdpa_kernel(to_gpu(q), cache, 0.3, out_dtype=torch.float32)
-    assert_close(out32[0].cpu().numpy(), fused, 2e-5, 1e-5)
+    assert_close(out32[0].cpu().numpy(), fused, 5e-5, 2.5e-4)
+    out32g = chronoquant_sdpa_kernel(to_gpu(q), cache, 0.3, out_dtype=torch.float32, generic=True)
+    assert_close(out32g[0].cpu().numpy(), fused, 2e-5, 1e-5)  # portable kernel: fp32 weights
     # fp32 queries: q*scale is not rounded to fp16; compare with binary64
     # attention on the reconstruction
     outq = chronoquant_sdpa_kernel(to_gpu(q, torch.float32), cache, 0.3).cpu().numpy()
