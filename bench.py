@@ -90,6 +90,65 @@ def time_graph(launch_fns, steps, warmup, stream):
     return e0.elapsed_time(e1) / steps  # ms per launch
 
 
+def time_eager(launch_fns, steps, warmup, stream):
+    """Launch `steps` times (cycling launch_fns) without a graph, bracketed by
+    events on `stream` (for profilers that count per dispatch)."""
+    import torch
+    n = len(launch_fns)
+    with torch.cuda.stream(stream):
+        for i in range(max(warmup, 1)):
+            launch_fns[i % n]()
+        torch.cuda.synchronize()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for i in range(steps):
+            launch_fns[i % n]()
+        e1.record(stream)
+    e1.synchronize()
+    return e0.elapsed_time(e1) / steps
+
+
+def copy_calibration(dev, nbytes=256 << 20, reps=4):
+    """Plain device copies of known size: the reference reading of the
+    FETCH_SIZE / WRITE_SIZE counters (each copy reads and writes nbytes)."""
+    import torch
+    src = torch.empty(nbytes // 2, dtype=torch.float16, device=dev).fill_(1.0)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    for _ in range(reps):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    log(f"[bench] copy calibration: {reps} copies of {nbytes} bytes")
+
+
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "decode_mfma_c1_traffic.txt")
+
+
+def kernel_source_hash():
+    import hashlib
+    h = hashlib.sha256()
+    for f in ("cq_decode_mfma.hip", "cq_decode_common.h"):
+        with open(os.path.join(ROOT, "chronoquant_mlx_amd", "csrc", f), "rb") as fh:
+            h.update(fh.read())
+    return h.hexdigest()[:16]
+
+
+def measured_traffic(workload):
+    """HBM bytes per launch from the committed rocprofv3 --pmc summary, if it
+    was measured on the current kernel source and this workload."""
+    try:
+        with open(TRAFFIC_FILE) as fh:
+            kv = dict(line.split("=", 1) for line in fh.read().splitlines() if "=" in line
+                      and not line.startswith((" ", "#", "rocprofv3")))
+    except OSError:
+        return None
+    kv = {a.strip(): b.strip() for a, b in kv.items()}
+    if kv.get("kernel_source_sha256_16") != kernel_source_hash() or kv.get("workload") != workload:
+        return None
+    return int(kv["traffic_bytes_per_launch"])
+
+
 def cpu_baseline(cfg, k, v, q, budget_s=12.0):
     from oracle import oracle as O
     threads = min(16, len(os.sched_getaffinity(0)))
@@ -119,6 +178,10 @@ def main():
     ap.add_argument("--replicas", type=int, default=0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-fp16-baseline", action="store_true")
+    ap.add_argument("--eager", action="store_true",
+                    help="launch without a HIP graph (for rocprofv3 --pmc passes)")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="also run plain 256 MiB copies (counter scale reference)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on exactly one GPU; --gpus must be 1 "
@@ -158,7 +221,8 @@ def main():
         return f
 
     log(f"[bench] {reps} replicas x {cache.nbytes / 1e6:.1f} MB; timing {args.steps} steps")
-    ms = time_graph([mk(d) for d in descs], args.steps, args.warmup, stream)
+    timer = time_eager if args.eager else time_graph
+    ms = timer([mk(d) for d in descs], args.steps, args.warmup, stream)
     gbs = algo_bytes / (ms * 1e-3) / 1e9
     # correctness of the timed kernel against the eager call
     ref = chronoquant_sdpa_kernel(q, cache, scale)
@@ -177,7 +241,7 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f32",
+        "dtype": "f16",
         "data": "synthetic",
         "config": {"workload": f"{cfg.name}: B={cfg.B} GQA {cfg.n_q_heads}q/{cfg.n_kv_heads}kv "
                                f"D={cfg.head_dim} T={cfg.T} strides {cfg.stride_k}/{cfg.stride_v} "
@@ -185,8 +249,13 @@ def main():
                    "algorithmic_bytes_per_step": algo_bytes,
                    "replicas": reps},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None},
+                     "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
+                     "traffic": measured_traffic(cfg.name)},
     }
+    if args.eager:
+        result["config"]["launch"] = "eager"
+    if args.copy_calibration:
+        copy_calibration(dev)
 
     if not args.no_fp16_baseline:
         H, D, T = cfg.n_kv_heads, cfg.head_dim, cfg.T
@@ -205,7 +274,7 @@ def main():
                 assert st == 0, _lib.status_string(st)
             return f
 
-        ms16 = time_graph([mk16(a, b) for a, b in kvs], args.steps, args.warmup, stream)
+        ms16 = timer([mk16(a, b) for a, b in kvs], args.steps, args.warmup, stream)
         log(f"[bench] fp16 flash decode {ms16 * 1e3:.2f} us/layer")
         result["fp16_baseline"] = {"us_per_layer": round(ms16 * 1e3, 3),
                                    "GBps": round(fp16_bytes / (ms16 * 1e-3) / 1e9, 1),
