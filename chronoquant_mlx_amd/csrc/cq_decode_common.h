@@ -7,6 +7,7 @@
 #pragma once
 
 #include <hip/hip_runtime.h>
+#include <math.h>
 
 #include "cq_device.h"
 
@@ -74,39 +75,82 @@ __device__ __forceinline__ float load_dev(const float *p) {
   return __hip_atomic_load(const_cast<float *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// Buffer resource over [base, base + bytes): loads past the end return 0.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, (int)bytes,
+                                           0x00020000);
+}
+// Vector forms of the device-scope accesses above: the same sc1 cache policy
+// (cache-policy operand 16), 8 or 16 bytes per access.
+constexpr int kPolicyDevice = 16;
+typedef float f2v_t __attribute__((ext_vector_type(2)));
+typedef float f4v_t __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ f2v_t load_dev2(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_bit_cast(f2v_t, __builtin_amdgcn_raw_buffer_load_b64(r, (int)off, 0, kPolicyDevice));
+}
+__device__ __forceinline__ f4v_t load_dev4(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_bit_cast(f4v_t, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, kPolicyDevice));
+}
+__device__ __forceinline__ float load_dev1(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, (int)off, 0, kPolicyDevice));
+}
+__device__ __forceinline__ void store_dev2(__amdgpu_buffer_rsrc_t r, uint32_t off, f2v_t v) {
+  __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(
+      __attribute__((ext_vector_type(2))) int, v), r, (int)off, 0, kPolicyDevice);
+}
+__device__ __forceinline__ void store_dev4(__amdgpu_buffer_rsrc_t r, uint32_t off, f4v_t v) {
+  __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(
+      __attribute__((ext_vector_type(4))) int, v), r, (int)off, 0, kPolicyDevice);
+}
+__device__ __forceinline__ void store_dev1(__amdgpu_buffer_rsrc_t r, uint32_t off, float v) {
+  __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(int, v), r, (int)off, 0, kPolicyDevice);
+}
+
 // Per-workgroup epilogue.  The workgroup's merged state for q heads
 // j0 .. j0+gn-1 of kv head h is in LDS: wm[j] (running max, log2 units),
 // wl[j] (sum of weights), wo[j*ostride + d] (unnormalised output).  With one
 // split it writes the output; otherwise it writes a partial, and the last
 // workgroup of (b, h, chunk) to finish merges all partials and resets the
 // counter it used.  `scratch` (kCombineScratchFloats floats of LDS) may alias
-// wm/wl/wo: it is written only after they have been consumed.  The merge
-// issues its loads in batches before using them, so it costs about one
-// memory round trip per phase plus the partial bytes.
-constexpr int kCombineWeights = 4096;  // (m, l) pairs of a head batch: 2 x 2048
-constexpr int kCombineScratchFloats = kCombineWeights + 16 + 16 * 256;
+// wm/wl/wo: it is written only after they have been consumed.
+//
+// The merge costs one memory round trip: a thread owns (head, 4 dims) and a
+// slice of the splits, issues every load of its splits ((m, l) pairs and
+// 16-byte partial vectors) before using any, folds them with a running
+// log-sum-exp, and the slices of a unit are folded the same way through LDS.
+constexpr int kCombineScratchFloats = 6 * 1024 + 16;
+constexpr int kCombineBatch = 8;  // splits whose loads are in flight together
 
 __device__ __forceinline__ void finish_workgroup(const DecodeArgs &a, int b, int h, int chunk,
                                                  int j0, int gn, int split, const float *wm,
                                                  const float *wl, const float *wo, int ostride,
                                                  float *scratch) {
   const int tid = threadIdx.x, nthr = blockDim.x;
-  const bool direct = a.nsplit == 1;
-  for (int e = tid; e < gn * a.D; e += nthr) {
-    const int j = e / a.D, dim = e - j * a.D;
-    const int64_t bq = (int64_t)b * a.nq + h * a.G + j0 + j;
-    const float L = wl[j], O = wo[j * ostride + dim];
-    if (direct) {
-      store_any(a.out_dtype, a.out, bq * a.D + dim, L > 0.f ? O / L : 0.f);
-    } else {
-      store_dev(&a.part_acc[(bq * a.nsplit + split) * a.D + dim], O);
-      if (dim == 0) {
-        store_dev(&a.part_ml[(bq * a.nsplit + split) * 2 + 0], wm[j]);
-        store_dev(&a.part_ml[(bq * a.nsplit + split) * 2 + 1], L);
-      }
+  const int D = a.D, nd4 = (D + 3) / 4;
+  const bool vec = (D & 3) == 0;  // 16-byte partial accesses
+  const int64_t bq0 = (int64_t)b * a.nq + h * a.G + j0;
+  if (a.nsplit == 1) {
+    for (int e = tid; e < gn * D; e += nthr) {
+      const int j = e / D, dim = e - j * D;
+      const float L = wl[j], O = wo[j * ostride + dim];
+      store_any(a.out_dtype, a.out, (bq0 + j) * D + dim, L > 0.f ? O / L : 0.f);
     }
+    return;
   }
-  if (direct) return;
+  const int nsplit = a.nsplit;
+  // partials: (m, l) and o of this split, 16 bytes per access
+  for (int u = tid; u < gn * nd4; u += nthr) {
+    const int j = u / nd4, d0 = 4 * (u - j * nd4);
+    const int64_t row = (bq0 + j) * nsplit + split;
+    const __amdgpu_buffer_rsrc_t racc = make_rsrc(a.part_acc + row * D, (uint32_t)D * 4u);
+    const float *o = wo + j * ostride + d0;
+    if (vec) {
+      store_dev4(racc, 4u * d0, f4v_t{o[0], o[1], o[2], o[3]});
+    } else {
+      for (int c = 0; c < 4 && d0 + c < D; ++c) store_dev1(racc, 4u * (d0 + c), o[c]);
+    }
+    if (d0 == 0) store_dev2(make_rsrc(a.part_ml + row * 2, 8u), 0u, f2v_t{wm[j], wl[j]});
+  }
 
   __shared__ int s_last;
   __builtin_amdgcn_s_waitcnt(0);  // this thread's partial stores are complete
@@ -115,94 +159,97 @@ __device__ __forceinline__ void finish_workgroup(const DecodeArgs &a, int b, int
   if (tid == 0) {
     const uint32_t prev =
         __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    s_last = (prev == (uint32_t)(a.nsplit - 1));
+    s_last = (prev == (uint32_t)(nsplit - 1));
   }
   __syncthreads();
   if (!s_last) return;
-  __builtin_amdgcn_s_waitcnt(0);
 
-  // scratch: m -> weights [hb][nsplit] at the bottom, l [hb][nsplit] from
-  // kCombineWeights/2, 1/L [16], outputs [hb][D]
-  const int nsplit = a.nsplit;
-  const int wave = tid >> 6, lane = tid & 63, nwaves = nthr >> 6;
-  const int half = kCombineWeights / 2;
-  const int hb_max = max(1, min(16, half / nsplit));
-  float *s_wt = scratch;
-  float *s_l = scratch + half;
-  float *s_inv = scratch + kCombineWeights;
-  float *s_out = s_inv + 16;
-  const int64_t bq0 = (int64_t)b * a.nq + h * a.G + j0;
-  const int nd4 = (a.D + 3) / 4;
-  for (int jb = 0; jb < gn; jb += hb_max) {
-    const int hb = min(hb_max, gn - jb);
-    // (m, l) of every (head, split) of the batch, one load each
-    for (int e = tid; e < hb * nsplit; e += nthr) {
-      const int j = e / nsplit, sp = e - j * nsplit;
-      const float *ml = a.part_ml + ((bq0 + jb + j) * nsplit + sp) * 2;
-      s_wt[e] = load_dev(ml);
-      s_l[e] = load_dev(ml + 1);
-    }
-    for (int e = tid; e < hb * a.D; e += nthr) s_out[e] = 0.f;
-    __syncthreads();
-    // one wave per head: max, weights, 1 / sum of weighted l
-    for (int j = wave; j < hb; j += nwaves) {
-      float mx = -INFINITY;
-      for (int sp = lane; sp < nsplit; sp += 64) mx = fmaxf(mx, s_wt[j * nsplit + sp]);
-      mx = wave_max(mx);
-      float ls = 0.f;
-      for (int sp = lane; sp < nsplit; sp += 64) {
-        const float m = s_wt[j * nsplit + sp];
-        const float w = (mx == -INFINITY || m == -INFINITY) ? 0.f : fast_exp2(m - mx);
-        ls += w * s_l[j * nsplit + sp];
-        s_wt[j * nsplit + sp] = w;
-      }
-      ls = wave_sum(ls);
-      if (lane == 0) s_inv[j] = ls > 0.f ? 1.f / ls : 0.f;
-    }
-    __syncthreads();
-    // weighted sum of the partial outputs: a thread takes (head, 4 dims) and a
-    // slice of the splits; 8 splits' loads are in flight before they are used
-    const int units = hb * nd4;
-    const int slices = max(1, nthr / units);
-    const int slice = tid / units;
-    if (slice < slices) {
-      for (int u = tid % units; u < units; u += nthr) {
-        const int j = u / nd4, d0 = 4 * (u - j * nd4);
-        const int nc = min(4, a.D - d0);
-        const float *pa = a.part_acc + (bq0 + jb + j) * nsplit * a.D + d0;
-        float o[4] = {0.f, 0.f, 0.f, 0.f};
-        int sp = slice;
-        for (; sp + 7 * slices < nsplit; sp += 8 * slices) {
-          float v[8][4];
+  // ---- last workgroup: fold the nsplit partials of every (head, 4 dims) ----
+  const int units = gn * nd4;
+  const int slices = units >= nthr ? 1 : min(nsplit, nthr / units);
+  float *s_m = scratch;                        // [slices][units]
+  float *s_l = s_m + slices * units;           // [slices][units]
+  float *s_o = s_l + slices * units;           // [slices][units][4]
+  for (int t = tid; t < units * slices; t += nthr) {
+    const int u = t % units, sl = t / units;
+    const int j = u / nd4, d0 = 4 * (u - j * nd4);
+    const int64_t row0 = (bq0 + j) * nsplit;
+    const __amdgpu_buffer_rsrc_t rml = make_rsrc(a.part_ml + row0 * 2, (uint32_t)nsplit * 8u);
+    const __amdgpu_buffer_rsrc_t racc =
+        make_rsrc(a.part_acc + row0 * D, (uint32_t)nsplit * (uint32_t)D * 4u);
+    float M = -INFINITY, L = 0.f;
+    float o[4] = {0.f, 0.f, 0.f, 0.f};
+    for (int sp0 = sl; sp0 < nsplit; sp0 += kCombineBatch * slices) {
+      f2v_t ml[kCombineBatch];
+      f4v_t ov[kCombineBatch];
 #pragma unroll
-          for (int k = 0; k < 8; ++k)
-#pragma unroll
-            for (int c = 0; c < 4; ++c)
-              v[k][c] = c < nc ? load_dev(pa + (int64_t)(sp + k * slices) * a.D + c) : 0.f;
-#pragma unroll
-          for (int k = 0; k < 8; ++k) {
-            const float w = s_wt[j * nsplit + sp + k * slices];
-#pragma unroll
-            for (int c = 0; c < 4; ++c) o[c] += w * v[k][c];
-          }
+      for (int k = 0; k < kCombineBatch; ++k) {
+        // splits past the end read past the buffer (zeros) and are masked below
+        const int sp = sp0 + k * slices;
+        const uint32_t spo = (uint32_t)min(sp, nsplit);
+        ml[k] = load_dev2(rml, spo * 8u);
+        const uint32_t off = (spo * (uint32_t)D + (uint32_t)d0) * 4u;
+        if (vec) {
+          ov[k] = load_dev4(racc, off);
+        } else {
+          ov[k] = f4v_t{load_dev1(racc, off), d0 + 1 < D ? load_dev1(racc, off + 4u) : 0.f,
+                        d0 + 2 < D ? load_dev1(racc, off + 8u) : 0.f,
+                        d0 + 3 < D ? load_dev1(racc, off + 12u) : 0.f};
         }
-        for (; sp < nsplit; sp += slices) {
-          const float w = s_wt[j * nsplit + sp];
-#pragma unroll
-          for (int c = 0; c < 4; ++c)
-            if (c < nc) o[c] += w * load_dev(pa + (int64_t)sp * a.D + c);
-        }
-#pragma unroll
-        for (int c = 0; c < 4; ++c)
-          if (c < nc) atomicAdd(&s_out[j * a.D + d0 + c], o[c]);
       }
+      float mb = M;
+#pragma unroll
+      for (int k = 0; k < kCombineBatch; ++k) {
+        if (sp0 + k * slices >= nsplit) ml[k].x = -INFINITY;
+        mb = fmaxf(mb, ml[k].x);
+      }
+      if (mb == -INFINITY) continue;
+      const float f = (M == -INFINITY) ? 0.f : fast_exp2(M - mb);
+      L *= f;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) o[c] *= f;
+#pragma unroll
+      for (int k = 0; k < kCombineBatch; ++k) {
+        const float w = (ml[k].x == -INFINITY) ? 0.f : fast_exp2(ml[k].x - mb);
+        L += w * ml[k].y;
+        o[0] += w * ov[k].x;
+        o[1] += w * ov[k].y;
+        o[2] += w * ov[k].z;
+        o[3] += w * ov[k].w;
+      }
+      M = mb;
     }
-    __syncthreads();
-    for (int e = tid; e < hb * a.D; e += nthr) {
-      const int j = e / a.D, dim = e - j * a.D;
-      store_any(a.out_dtype, a.out, (bq0 + jb + j) * a.D + dim, s_out[e] * s_inv[j]);
+    if (slices == 1) {
+      const float inv = L > 0.f ? 1.f / L : 0.f;
+      for (int c = 0; c < 4 && d0 + c < D; ++c)
+        store_any(a.out_dtype, a.out, (bq0 + j) * D + d0 + c, o[c] * inv);
+    } else {
+      s_m[t] = M;
+      s_l[t] = L;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) s_o[4 * t + c] = o[c];
     }
+  }
+  if (slices > 1) {
     __syncthreads();
+    for (int u = tid; u < units; u += nthr) {
+      const int j = u / nd4, d0 = 4 * (u - j * nd4);
+      float M = -INFINITY;
+      for (int sl = 0; sl < slices; ++sl) M = fmaxf(M, s_m[sl * units + u]);
+      float L = 0.f, o[4] = {0.f, 0.f, 0.f, 0.f};
+      if (M != -INFINITY) {
+        for (int sl = 0; sl < slices; ++sl) {
+          const int t = sl * units + u;
+          const float w = (s_m[t] == -INFINITY) ? 0.f : fast_exp2(s_m[t] - M);
+          L += w * s_l[t];
+#pragma unroll
+          for (int c = 0; c < 4; ++c) o[c] += w * s_o[4 * t + c];
+        }
+      }
+      const float inv = L > 0.f ? 1.f / L : 0.f;
+      for (int c = 0; c < 4 && d0 + c < D; ++c)
+        store_any(a.out_dtype, a.out, (bq0 + j) * D + d0 + c, o[c] * inv);
+    }
   }
   if (tid == 0) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
@@ -273,6 +320,7 @@ inline int prepare_launch(DecodeArgs &a, int chunk_heads, void *workspace, size_
   if (a.nsplit > 1) {
     if ((int64_t)a.B * a.H * a.n_chunks > kMaxCounters) return CQ_ERR_UNSUPPORTED;
     if (!workspace) return CQ_ERR_WORKSPACE;
+    if ((uintptr_t)workspace & 255) return CQ_ERR_ALIGN;
     if (ws_bytes < workspace_bytes_for(a.B, a.nq, a.D, a.nsplit)) return CQ_ERR_WORKSPACE;
     carve_workspace(a, workspace);
   } else {

@@ -71,10 +71,6 @@ __device__ __forceinline__ uint32_t and_or(uint32_t x, uint32_t m, uint32_t o) {
   return (x & m) | o;
 }
 
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *base, uint32_t bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, (int)bytes,
-                                           0x00020000);
-}
 __device__ __forceinline__ uint32_t bload32(__amdgpu_buffer_rsrc_t r, uint32_t off) {
   return (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(r, (int)off, 0, 0);
 }
@@ -141,7 +137,10 @@ struct alignas(16) WaveScratch {
   float qa[kChunk][kHeads];            // q'.anchor_k by (local anchor, head)
 };
 
+constexpr int kMergeHeads = 8;  // q heads per merge pass
+
 struct MergeScratch {
+  float t[kWaves][kMergeHeads][kD];  // each wave's unnormalised output tile
   float m[kWaves][kHeads], l[kWaves][kHeads];
   float wm[kHeads], wl[kHeads];
   float o[kHeads][kD];
@@ -155,6 +154,10 @@ union DecodeLds {
 
 // Merge the 8 waves' (m, l, o) through LDS and run the split epilogue.
 // o_val(nb, r) is this lane's unnormalised output for head 4kg+r, dim 8col+nb.
+// Each wave stores its tile with 16-byte writes (lane col owns dims
+// 8col..8col+7 of its 4 heads); after one barrier every thread sums the 8
+// tiles of (head, 4 dims) with the log-sum-exp weights, reading the 8 waves'
+// running maxima itself.  Up to kMergeHeads heads per pass.
 template <typename OVal>
 __device__ __forceinline__ void merge_and_finish(const DecodeArgs &a, DecodeLds &lds, int b,
                                                  int h, int chunk, int j0, int gn, int split,
@@ -163,34 +166,51 @@ __device__ __forceinline__ void merge_and_finish(const DecodeArgs &a, DecodeLds 
   const int col = lane & 15, kg = lane >> 4;
   __syncthreads();  // wave scratch becomes the merge area
   MergeScratch &M = lds.mg;
-  for (int e = tid; e < kHeads * kD; e += kThreadsMfma) (&M.o[0][0])[e] = 0.f;
   if (kg == 0) {
     M.m[wave][col] = m_run;
     M.l[wave][col] = l_run;
   }
-  __syncthreads();
-  if (tid < kHeads) {
-    float mm = -INFINITY;
-    for (int wv = 0; wv < kWaves; ++wv) mm = fmaxf(mm, M.m[wv][tid]);
-    float L = 0.f;
-    if (mm != -INFINITY)
-      for (int wv = 0; wv < kWaves; ++wv)
-        if (M.m[wv][tid] != -INFINITY) L += M.l[wv][tid] * fast_exp2(M.m[wv][tid] - mm);
-    M.wm[tid] = mm;
-    M.wl[tid] = L;
-  }
-  __syncthreads();
+  for (int p0 = 0; p0 < gn; p0 += kMergeHeads) {
+    const int pn = min(kMergeHeads, gn - p0);
 #pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    const int hh = 4 * kg + r;
-    const float mw = __shfl(m_run, hh, 64);
-    if (hh < gn && mw != -INFINITY) {
-      const float f = fast_exp2(mw - M.wm[hh]);
-#pragma unroll
-      for (int nb = 0; nb < 8; ++nb) atomicAdd(&M.o[hh][8 * col + nb], o_val(nb, r) * f);
+    for (int r = 0; r < 4; ++r) {
+      const int hp = 4 * kg + r - p0;
+      if (hp >= 0 && hp < pn) {
+        float4 *dst = (float4 *)&M.t[wave][hp][8 * col];
+        dst[0] = make_float4(o_val(0, r), o_val(1, r), o_val(2, r), o_val(3, r));
+        dst[1] = make_float4(o_val(4, r), o_val(5, r), o_val(6, r), o_val(7, r));
+      }
     }
+    __syncthreads();
+    for (int e = tid; e < pn * (kD / 4); e += kThreadsMfma) {
+      const int hp = e / (kD / 4), d0 = 4 * (e - hp * (kD / 4));
+      const int hh = p0 + hp;
+      float mw[kWaves], mm = -INFINITY;
+#pragma unroll
+      for (int w = 0; w < kWaves; ++w) {
+        mw[w] = M.m[w][hh];
+        mm = fmaxf(mm, mw[w]);
+      }
+      float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
+      float L = 0.f;
+#pragma unroll
+      for (int w = 0; w < kWaves; ++w) {
+        const float f = (mw[w] == -INFINITY) ? 0.f : fast_exp2(mw[w] - mm);
+        const float4 t = *(const float4 *)&M.t[w][hp][d0];
+        o.x += f * t.x;
+        o.y += f * t.y;
+        o.z += f * t.z;
+        o.w += f * t.w;
+        L += f * M.l[w][hh];
+      }
+      *(float4 *)&M.o[hh][d0] = o;
+      if (d0 == 0) {
+        M.wm[hh] = mm;
+        M.wl[hh] = L;
+      }
+    }
+    __syncthreads();
   }
-  __syncthreads();
   finish_workgroup(a, b, h, chunk, j0, gn, split, M.wm, M.wl, &M.o[0][0], kD, lds.combine);
 }
 
@@ -226,27 +246,15 @@ __global__ __launch_bounds__(kThreadsMfma) void decode_mfma_kernel(DecodeArgs a)
   const __amdgpu_buffer_rsrc_t r_sck = make_rsrc(a.sc[0] + bh * a.cap_pf[0], (uint32_t)(a.cap_pf[0] * 2));
   const __amdgpu_buffer_rsrc_t r_scv = make_rsrc(a.sc[1] + bh * a.cap_pf[1], (uint32_t)(a.cap_pf[1] * 2));
 
-  // q'^T operand in the K order (dims 32kg + 8kb + {0,4,1,5,2,6,3,7}); columns
-  // >= gn are zero.  s8 = 8 * sum_d q'_d of head col.
-  h8_t qc[4];
-  float s8;
+  // raw q rows of head col, dims 32kg .. 32kg+31 (converted after the first
+  // chunk's loads are issued, so the two round trips overlap)
+  const bool qok = col < gn;
+  uint4 qraw[4];
   {
-    const bool qok = col < gn;
-    const _Float16 sc16 = qok ? (_Float16)a.scale : (_Float16)0.f;
     const uint16_t *qrow =
         (const uint16_t *)a.q + ((int64_t)b * a.nq + h * a.G + j0 + (qok ? col : 0)) * kD + 32 * kg;
-    uint4 u[4];
 #pragma unroll
-    for (int kb = 0; kb < 4; ++kb) u[kb] = *(const uint4 *)(qrow + 8 * kb);
-    float qs = 0.f;
-#pragma unroll
-    for (int kb = 0; kb < 4; ++kb) {
-      const h8_t v = __builtin_bit_cast(h8_t, u[kb]) * sc16;  // fp16(q * fp16(scale))
-      qc[kb] = h8_t{v[0], v[4], v[1], v[5], v[2], v[6], v[3], v[7]};
-#pragma unroll
-      for (int e = 0; e < 8; ++e) qs += (float)v[e];
-    }
-    s8 = 8.f * shfl_sum_kg(qs);
+    for (int kb = 0; kb < 4; ++kb) qraw[kb] = *(const uint4 *)(qrow + 8 * kb);
   }
   uint32_t magic;  // fp16 1024 in both halves, held in a VGPR for v_and_or_b32
   asm volatile("v_mov_b32 %0, 0x64006400" : "=v"(magic));
@@ -262,15 +270,17 @@ __global__ __launch_bounds__(kThreadsMfma) void decode_mfma_kernel(DecodeArgs a)
   const h2_t sixteenth = {(_Float16)0.0625f, (_Float16)0.0625f};
 
   WaveScratch &W = lds.w[wave];
-  for (int64_t c0l = t0 + (int64_t)wave * kChunk; c0l < t1; c0l += kWaves * kChunk) {
-    const int c0 = (int)c0l;
-    const int nt = (int)min((int64_t)kChunk, t1 - c0l);
+  int nt = 0;  // valid tokens of the staged chunk
+  uint4 ka[4], kw[4], va[4];
+  uint32_t vw[4][4];
+  // Stage the chunk at c0: token table to LDS, then every load of the chunk.
+  auto stage = [&](int c0) {
+    nt = (int)min((int64_t)kChunk, t1 - c0);
     const int gk_base = div_stride(c0, sk, isk);
     const int gk_last = div_stride(c0 + nt - 1, sk, isk);
     const int gv_base = div_stride(c0, sv, isv);
     const int gv_last = div_stride(c0 + nt - 1, sv, isv);
-
-    // ---- token phase: one token per lane; scale loads first --------------------
+    // token phase: one token per lane; scale loads first
     uint32_t s16;
     {
       const bool valid = lane < nt;
@@ -288,10 +298,6 @@ __global__ __launch_bounds__(kThreadsMfma) void decode_mfma_kernel(DecodeArgs a)
       s16 = sk16 | (sv16 << 16);
     }
     wave_lds_sync();
-
-    // ---- issue the chunk's loads -------------------------------------------------
-    uint4 ka[4], kw[4], va[4];
-    uint32_t vw[4][4];
     {
       // anchor row gk_base + col, dims 32kg + 8kb .. +7 (the dims qc[kb] holds)
       const uint32_t row = (uint32_t)min(gk_base + col, gk_last) * 256u + 64u * kg;
@@ -315,7 +321,29 @@ __global__ __launch_bounds__(kThreadsMfma) void decode_mfma_kernel(DecodeArgs a)
     for (int r = 0; r < 4; ++r)
       va[r] = bload128(r_kfv, (uint32_t)min(gv_base + 4 * kg + r, gv_last) * 256u + 16u * col);
     W.s16[lane] = s16;
+  };
 
+  int64_t c0l = t0 + (int64_t)wave * kChunk;
+  if (c0l < t1) stage((int)c0l);
+
+  // q'^T operand in the K order (dims 32kg + 8kb + {0,4,1,5,2,6,3,7}); columns
+  // >= gn are zero.  s8 = 8 * sum_d q'_d of head col.
+  h8_t qc[4];
+  float s8;
+  {
+    const _Float16 sc16 = qok ? (_Float16)a.scale : (_Float16)0.f;
+    float qs = 0.f;
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb) {
+      const h8_t v = __builtin_bit_cast(h8_t, qraw[kb]) * sc16;  // fp16(q * fp16(scale))
+      qc[kb] = h8_t{v[0], v[4], v[1], v[5], v[2], v[6], v[3], v[7]};
+#pragma unroll
+      for (int e = 0; e < 8; ++e) qs += (float)v[e];
+    }
+    s8 = 8.f * shfl_sum_kg(qs);
+  }
+
+  while (c0l < t1) {
     // ---- q'.anchor table (anchor gk_base + 4kg + r, head col) ---------------------
     {
       f4_t d = {0.f, 0.f, 0.f, 0.f};
@@ -429,6 +457,8 @@ __global__ __launch_bounds__(kThreadsMfma) void decode_mfma_kernel(DecodeArgs a)
       }
     }
     wave_lds_sync();
+    c0l += kWaves * kChunk;
+    if (c0l < t1) stage((int)c0l);
   }
 
   // ---- totals: the 4 lane groups of a column hold disjoint tokens ---------------

@@ -1,7 +1,7 @@
 /*
  * chronoquant.h — C ABI of the MI355X (gfx950) ChronoQuant KV-cache hot path.
  *
- * The library is libchronoquant.so (built from chronoquant_mlx_amd/csrc/*.hip).
+ * The library is libchronoquant.so, built from the .hip sources in chronoquant_mlx_amd/csrc.
  * Every entry point:
  *   - returns an int status (CQ_OK == 0); no exception ever crosses the ABI;
  *   - takes caller-owned DEVICE pointers (the library never allocates device
@@ -120,7 +120,7 @@ int cq_reconstruct(const cq_cache_desc *cache, int32_t component,
  * split counters (one per sequence x kv head x q-head chunk, at most 16384),
  * which every call returns to zero, so one workspace can be reused — also by
  * calls of other shapes — without clearing.  Calls that share a workspace
- * must be ordered on one stream. */
+ * must be ordered on one stream.  The workspace must be 256-byte aligned. */
 size_t cq_decode_workspace_size(int32_t batch, int32_t n_kv_heads,
                                 int32_t n_q_heads, int32_t head_dim,
                                 int64_t max_seq_len);
