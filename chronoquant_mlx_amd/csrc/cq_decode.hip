@@ -160,7 +160,7 @@ __global__ __launch_bounds__(256) void decode_generic_kernel(DecodeArgs a) {
   __shared__ float s_m[4][kGenericGroup], s_l[4][kGenericGroup];
   // the combine scratch aliases the wave accumulators once they are merged
   constexpr int kAccFloats = 4 * kGenericGroup * kMaxHeadDim;
-  __shared__ float s_acc_raw[kAccFloats > kCombineScratchFloats ? kAccFloats : kCombineScratchFloats];
+  __shared__ float s_acc_raw[kAccFloats];
   float(*s_acc)[kGenericGroup][kMaxHeadDim] = (float(*)[kGenericGroup][kMaxHeadDim])s_acc_raw;
   __shared__ float w_m[kGenericGroup], w_l[kGenericGroup];
   if (sub == 0) {
@@ -195,8 +195,7 @@ __global__ __launch_bounds__(256) void decode_generic_kernel(DecodeArgs a) {
     s_acc[0][j][dim] = O;  // each (j, dim) is read and rewritten by one thread
   }
   __syncthreads();
-  finish_workgroup(a, b, h, chunk, j0, gn, split, w_m, w_l, &s_acc[0][0][0], kMaxHeadDim,
-                   s_acc_raw);
+  finish_workgroup(a, b, h, chunk, j0, gn, split, w_m, w_l, &s_acc[0][0][0], kMaxHeadDim);
 }
 
 // ---------------------------------------------------------------------------

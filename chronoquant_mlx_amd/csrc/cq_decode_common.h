@@ -85,6 +85,7 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *base, ui
 constexpr int kPolicyDevice = 16;
 typedef float f2v_t __attribute__((ext_vector_type(2)));
 typedef float f4v_t __attribute__((ext_vector_type(4)));
+typedef _Float16 h2v_t __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ f2v_t load_dev2(__amdgpu_buffer_rsrc_t r, uint32_t off) {
   return __builtin_bit_cast(f2v_t, __builtin_amdgcn_raw_buffer_load_b64(r, (int)off, 0, kPolicyDevice));
 }
@@ -111,20 +112,19 @@ __device__ __forceinline__ void store_dev1(__amdgpu_buffer_rsrc_t r, uint32_t of
 // wl[j] (sum of weights), wo[j*ostride + d] (unnormalised output).  With one
 // split it writes the output; otherwise it writes a partial, and the last
 // workgroup of (b, h, chunk) to finish merges all partials and resets the
-// counter it used.  `scratch` (kCombineScratchFloats floats of LDS) may alias
-// wm/wl/wo: it is written only after they have been consumed.
+// counter it used.
 //
 // The merge costs one memory round trip: a thread owns (head, 4 dims) and a
 // slice of the splits, issues every load of its splits ((m, l) pairs and
 // 16-byte partial vectors) before using any, folds them with a running
-// log-sum-exp, and the slices of a unit are folded the same way through LDS.
-constexpr int kCombineScratchFloats = 6 * 1024 + 16;
+// log-sum-exp, and the slices of a unit (adjacent lanes) are folded the same
+// way with xor shuffles.
 constexpr int kCombineBatch = 8;  // splits whose loads are in flight together
 
 __device__ __forceinline__ void finish_workgroup(const DecodeArgs &a, int b, int h, int chunk,
                                                  int j0, int gn, int split, const float *wm,
-                                                 const float *wl, const float *wo, int ostride,
-                                                 float *scratch) {
+                                                 const float *wl, const float *wo,
+                                                 int ostride) {
   const int tid = threadIdx.x, nthr = blockDim.x;
   const int D = a.D, nd4 = (D + 3) / 4;
   const bool vec = (D & 3) == 0;  // 16-byte partial accesses
@@ -165,14 +165,18 @@ __device__ __forceinline__ void finish_workgroup(const DecodeArgs &a, int b, int
   if (!s_last) return;
 
   // ---- last workgroup: fold the nsplit partials of every (head, 4 dims) ----
+  // A unit's `slices` threads are adjacent lanes (slices a power of two <= 64),
+  // so the slices fold with xor shuffles: no LDS, no barrier.
   const int units = gn * nd4;
-  const int slices = units >= nthr ? 1 : min(nsplit, nthr / units);
-  float *s_m = scratch;                        // [slices][units]
-  float *s_l = s_m + slices * units;           // [slices][units]
-  float *s_o = s_l + slices * units;           // [slices][units][4]
-  for (int t = tid; t < units * slices; t += nthr) {
-    const int u = t % units, sl = t / units;
-    const int j = u / nd4, d0 = 4 * (u - j * nd4);
+  int slices = 1;
+  while (slices * 2 <= nsplit && units * slices * 2 <= nthr && slices < 64) slices *= 2;
+  const int rounds = (units * slices + nthr - 1) / nthr;
+  for (int rd = 0; rd < rounds; ++rd) {
+    const int t = rd * nthr + tid;
+    const int u = t / slices, sl = t - u * slices;
+    const bool live = u < units;  // whole slice groups are live together
+    const int uu = live ? u : 0;
+    const int j = uu / nd4, d0 = 4 * (uu - j * nd4);
     const int64_t row0 = (bq0 + j) * nsplit;
     const __amdgpu_buffer_rsrc_t rml = make_rsrc(a.part_ml + row0 * 2, (uint32_t)nsplit * 8u);
     const __amdgpu_buffer_rsrc_t racc =
@@ -185,8 +189,7 @@ __device__ __forceinline__ void finish_workgroup(const DecodeArgs &a, int b, int
 #pragma unroll
       for (int k = 0; k < kCombineBatch; ++k) {
         // splits past the end read past the buffer (zeros) and are masked below
-        const int sp = sp0 + k * slices;
-        const uint32_t spo = (uint32_t)min(sp, nsplit);
+        const uint32_t spo = (uint32_t)min(sp0 + k * slices, nsplit);
         ml[k] = load_dev2(rml, spo * 8u);
         const uint32_t off = (spo * (uint32_t)D + (uint32_t)d0) * 4u;
         if (vec) {
@@ -219,36 +222,29 @@ __device__ __forceinline__ void finish_workgroup(const DecodeArgs &a, int b, int
       }
       M = mb;
     }
-    if (slices == 1) {
-      const float inv = L > 0.f ? 1.f / L : 0.f;
-      for (int c = 0; c < 4 && d0 + c < D; ++c)
-        store_any(a.out_dtype, a.out, (bq0 + j) * D + d0 + c, o[c] * inv);
-    } else {
-      s_m[t] = M;
-      s_l[t] = L;
+    // fold the slices of the unit (adjacent lanes)
+    float Mx = M;
+    for (int x = 1; x < slices; x *= 2) Mx = fmaxf(Mx, __shfl_xor(Mx, x, 64));
+    const float f = (M == -INFINITY) ? 0.f : fast_exp2(M - Mx);
+    L *= f;
 #pragma unroll
-      for (int c = 0; c < 4; ++c) s_o[4 * t + c] = o[c];
+    for (int c = 0; c < 4; ++c) o[c] *= f;
+    for (int x = 1; x < slices; x *= 2) {
+      L += __shfl_xor(L, x, 64);
+#pragma unroll
+      for (int c = 0; c < 4; ++c) o[c] += __shfl_xor(o[c], x, 64);
     }
-  }
-  if (slices > 1) {
-    __syncthreads();
-    for (int u = tid; u < units; u += nthr) {
-      const int j = u / nd4, d0 = 4 * (u - j * nd4);
-      float M = -INFINITY;
-      for (int sl = 0; sl < slices; ++sl) M = fmaxf(M, s_m[sl * units + u]);
-      float L = 0.f, o[4] = {0.f, 0.f, 0.f, 0.f};
-      if (M != -INFINITY) {
-        for (int sl = 0; sl < slices; ++sl) {
-          const int t = sl * units + u;
-          const float w = (s_m[t] == -INFINITY) ? 0.f : fast_exp2(s_m[t] - M);
-          L += w * s_l[t];
-#pragma unroll
-          for (int c = 0; c < 4; ++c) o[c] += w * s_o[4 * t + c];
-        }
-      }
+    if (live && sl == 0) {
       const float inv = L > 0.f ? 1.f / L : 0.f;
-      for (int c = 0; c < 4 && d0 + c < D; ++c)
-        store_any(a.out_dtype, a.out, (bq0 + j) * D + d0 + c, o[c] * inv);
+      const int64_t oi = (bq0 + j) * D + d0;
+      if (a.out_dtype == CQ_F16 && vec) {
+        const h2v_t lo = h2v_t{(_Float16)(o[0] * inv), (_Float16)(o[1] * inv)};
+        const h2v_t hi = h2v_t{(_Float16)(o[2] * inv), (_Float16)(o[3] * inv)};
+        *(uint2 *)((uint16_t *)a.out + oi) =
+            uint2{__builtin_bit_cast(uint32_t, lo), __builtin_bit_cast(uint32_t, hi)};
+      } else {
+        for (int c = 0; c < 4 && d0 + c < D; ++c) store_any(a.out_dtype, a.out, oi + c, o[c] * inv);
+      }
     }
   }
   if (tid == 0) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);

@@ -13,12 +13,15 @@
 //   summation and q'.c = 2^24 * raw - 8 * sum(q').  q'.a: the same with 16
 //   K anchor rows as A, kept in a per-wave LDS table.
 // * The score tile's output layout (lane = q head, 4 consecutive tokens) is
-//   the A- and the B-operand layout of v_mfma_f32_16x16x16_f16, so:
+//   the A- and the B-operand layout of the MFMA K index, and two 16-token
+//   tiles fill one K=32 product (gfx950 issues v_mfma_f32_16x16x32_f16 at the
+//   cost of the 16x16x16 form, so every product here is K=32):
 //   - (p*s) against the V codes, nibbles as fp16 1024+n (even dims) or
 //     1024+16n (odd dims, weighted by p*s/16), the constants removed at the
 //     end with sum(p s) and sum(p s / 16);
 //   - P_g^T = E^T p^T with E the 0/1 token->group matrix, accumulated over a
-//     64-token chunk, then P_g (an fp16 hi/lo pair) against the V anchors.
+//     64-token chunk, then P_g (an fp16 hi/lo pair in one K=32 operand)
+//     against the V anchors.
 //   Code and anchor terms share one fp32 accumulator tile per 16 dims.
 // Softmax in the log2 domain with a lazy running max per 64-token chunk
 // (rescale only when the chunk max exceeds it by more than 2^8), so the fp16
@@ -85,9 +88,6 @@ __device__ __forceinline__ uint32_t bload16(__amdgpu_buffer_rsrc_t r, uint32_t o
 __device__ __forceinline__ f4_t mfma32(h8_t a, h8_t b, f4_t c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }
-__device__ __forceinline__ f4_t mfma16(h4_t a, h4_t b, f4_t c) {
-  return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0);
-}
 
 __device__ __forceinline__ void wave_lds_sync() {
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -130,11 +130,22 @@ __device__ __forceinline__ h4_t rows_operand(const uint4 (&u)[4], int k, bool od
   return h4_of(__builtin_amdgcn_perm(w1, w0, sel), __builtin_amdgcn_perm(w3, w2, sel));
 }
 
+// Per-wave LDS.  The token tables of two chunks are live at once (the one
+// being computed and the one whose loads are in flight): index [buffer].
 struct alignas(16) WaveScratch {
-  int slot_k[kChunk], slot_v[kChunk];  // P-frame slot (-1: I-frame / padding)
-  int gkl[kChunk], gvl[kChunk];        // anchor index relative to the chunk's first
-  uint32_t s16[kChunk];                // fp16 K scale | fp16 V scale << 16 (0: none)
-  float qa[kChunk][kHeads];            // q'.anchor_k by (local anchor, head)
+  int slot_k[kChunk], slot_v[kChunk];  // P-frame slot (-1: I-frame / padding), staging only
+  int gkl[2][kChunk], gvl[2][kChunk];  // anchor index relative to the chunk's first
+  uint32_t s16[2][kChunk];             // fp16 K scale | fp16 V scale << 16 (0: none)
+  float qa[16][kHeads];                // q'.anchor_k by (local anchor, head)
+};
+
+// The registers one chunk's loads land in (the V anchor rows, used last, are
+// single-buffered and reloaded right after their use).
+struct ChunkBuf {
+  uint4 ka[4];        // K anchor row gk_base + col, dims 32kg + 8kb .. +7
+  uint4 kw[4];        // K code words 4kg..4kg+3 of token 16i + col
+  uint32_t vw[4][4];  // V code word col of token 16i + 4kg + r
+  int nt;             // valid tokens (0: nothing to compute)
 };
 
 constexpr int kMergeHeads = 8;  // q heads per merge pass
@@ -149,7 +160,6 @@ struct MergeScratch {
 union DecodeLds {
   WaveScratch w[kWaves];
   MergeScratch mg;
-  float combine[kCombineScratchFloats];
 };
 
 // Merge the 8 waves' (m, l, o) through LDS and run the split epilogue.
@@ -211,7 +221,7 @@ __device__ __forceinline__ void merge_and_finish(const DecodeArgs &a, DecodeLds 
     }
     __syncthreads();
   }
-  finish_workgroup(a, b, h, chunk, j0, gn, split, M.wm, M.wl, &M.o[0][0], kD, lds.combine);
+  finish_workgroup(a, b, h, chunk, j0, gn, split, M.wm, M.wl, &M.o[0][0], kD);
 }
 
 // ---------------------------------------------------------------------------
@@ -270,21 +280,22 @@ __global__ __launch_bounds__(kThreadsMfma) void decode_mfma_kernel(DecodeArgs a)
   const h2_t sixteenth = {(_Float16)0.0625f, (_Float16)0.0625f};
 
   WaveScratch &W = lds.w[wave];
-  int nt = 0;  // valid tokens of the staged chunk
-  uint4 ka[4], kw[4], va[4];
-  uint32_t vw[4][4];
-  // Stage the chunk at c0: token table to LDS, then every load of the chunk.
-  auto stage = [&](int c0) {
-    nt = (int)min((int64_t)kChunk, t1 - c0);
+  // Stage the chunk at c0 into cb and token-table buffer sl: token table to
+  // LDS, then every load of the chunk.  A chunk past the end (nt = 0) gets
+  // offsets past every buffer, so its loads return zeros without traffic.
+  auto stage = [&](int c0, ChunkBuf &cb, int sl) {
+    const int nt = (int)max((int64_t)0, min((int64_t)kChunk, t1 - c0));
+    cb.nt = nt;
     const int gk_base = div_stride(c0, sk, isk);
-    const int gk_last = div_stride(c0 + nt - 1, sk, isk);
+    const int gk_last = nt ? div_stride(c0 + nt - 1, sk, isk) : gk_base;
     const int gv_base = div_stride(c0, sv, isv);
-    const int gv_last = div_stride(c0 + nt - 1, sv, isv);
+    // anchor offsets stay below 2^30; buffers are below 2^31 bytes (mfma_supported)
+    const uint32_t dead = nt ? 0u : 0x80000000u;
     // token phase: one token per lane; scale loads first
     uint32_t s16;
     {
       const bool valid = lane < nt;
-      const int t = c0 + (valid ? lane : nt - 1);
+      const int t = c0 + (valid ? lane : max(nt - 1, 0));
       const int gk = div_stride(t, sk, isk), gv = div_stride(t, sv, isv);
       const int slk = (valid && t != gk * sk) ? t - gk - 1 : -1;
       const int slv = (valid && t != gv * sv) ? t - gv - 1 : -1;
@@ -293,44 +304,48 @@ __global__ __launch_bounds__(kThreadsMfma) void decode_mfma_kernel(DecodeArgs a)
       const uint32_t sv16 = bload16(r_scv, (uint32_t)slv * 2u);
       W.slot_k[lane] = slk;
       W.slot_v[lane] = slv;
-      W.gkl[lane] = gk - gk_base;
-      W.gvl[lane] = gv - gv_base;
+      W.gkl[sl][lane] = gk - gk_base;
+      W.gvl[sl][lane] = gv - gv_base;
       s16 = sk16 | (sv16 << 16);
     }
     wave_lds_sync();
     {
-      // anchor row gk_base + col, dims 32kg + 8kb .. +7 (the dims qc[kb] holds)
-      const uint32_t row = (uint32_t)min(gk_base + col, gk_last) * 256u + 64u * kg;
+      const uint32_t row = ((uint32_t)min(gk_base + col, gk_last) * 256u + 64u * kg) | dead;
 #pragma unroll
-      for (int kb = 0; kb < 4; ++kb) ka[kb] = bload128(r_kfk, row + 16u * kb);
+      for (int kb = 0; kb < 4; ++kb) cb.ka[kb] = bload128(r_kfk, row + 16u * kb);
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int slot = W.slot_k[16 * i + col];
-      kw[i] = bload128(r_pkk, (uint32_t)slot * 64u + 16u * kg);
+      cb.kw[i] = bload128(r_pkk, (uint32_t)slot * 64u + 16u * kg);
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int4 sl = *(const int4 *)&W.slot_v[16 * i + 4 * kg];
-      vw[i][0] = bload32(r_pkv, (uint32_t)sl.x * 64u + 4u * col);
-      vw[i][1] = bload32(r_pkv, (uint32_t)sl.y * 64u + 4u * col);
-      vw[i][2] = bload32(r_pkv, (uint32_t)sl.z * 64u + 4u * col);
-      vw[i][3] = bload32(r_pkv, (uint32_t)sl.w * 64u + 4u * col);
+      const int4 sl4 = *(const int4 *)&W.slot_v[16 * i + 4 * kg];
+      cb.vw[i][0] = bload32(r_pkv, (uint32_t)sl4.x * 64u + 4u * col);
+      cb.vw[i][1] = bload32(r_pkv, (uint32_t)sl4.y * 64u + 4u * col);
+      cb.vw[i][2] = bload32(r_pkv, (uint32_t)sl4.z * 64u + 4u * col);
+      cb.vw[i][3] = bload32(r_pkv, (uint32_t)sl4.w * 64u + 4u * col);
     }
+    W.s16[sl][lane] = s16;
+  };
+  // V anchor rows gv_base + 4kg + r of the chunk at c0, dims 8col .. 8col+7.
+  uint4 va[4];
+  auto stage_va = [&](int c0) {
+    const int nt = (int)max((int64_t)0, min((int64_t)kChunk, t1 - c0));
+    const int gv_base = div_stride(c0, sv, isv);
+    const int gv_last = nt ? div_stride(c0 + nt - 1, sv, isv) : gv_base;
+    const uint32_t dead = nt ? 0u : 0x80000000u;
 #pragma unroll
     for (int r = 0; r < 4; ++r)
-      va[r] = bload128(r_kfv, (uint32_t)min(gv_base + 4 * kg + r, gv_last) * 256u + 16u * col);
-    W.s16[lane] = s16;
+      va[r] = bload128(r_kfv, ((uint32_t)min(gv_base + 4 * kg + r, gv_last) * 256u + 16u * col) | dead);
   };
-
-  int64_t c0l = t0 + (int64_t)wave * kChunk;
-  if (c0l < t1) stage((int)c0l);
 
   // q'^T operand in the K order (dims 32kg + 8kb + {0,4,1,5,2,6,3,7}); columns
   // >= gn are zero.  s8 = 8 * sum_d q'_d of head col.
   h8_t qc[4];
-  float s8;
-  {
+  float s8 = 0.f;
+  auto prep_q = [&]() {
     const _Float16 sc16 = qok ? (_Float16)a.scale : (_Float16)0.f;
     float qs = 0.f;
 #pragma unroll
@@ -341,14 +356,15 @@ __global__ __launch_bounds__(kThreadsMfma) void decode_mfma_kernel(DecodeArgs a)
       for (int e = 0; e < 8; ++e) qs += (float)v[e];
     }
     s8 = 8.f * shfl_sum_kg(qs);
-  }
+  };
 
-  while (c0l < t1) {
+  // Compute the chunk staged in cb / token-table buffer sl.
+  auto compute = [&](ChunkBuf &cb, int sl) {
     // ---- q'.anchor table (anchor gk_base + 4kg + r, head col) ---------------------
     {
       f4_t d = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int kb = 0; kb < 4; ++kb) d = mfma32(korder(ka[kb]), qc[kb], d);
+      for (int kb = 0; kb < 4; ++kb) d = mfma32(korder(cb.ka[kb]), qc[kb], d);
 #pragma unroll
       for (int r = 0; r < 4; ++r) W.qa[4 * kg + r][col] = d[r];
     }
@@ -360,13 +376,13 @@ __global__ __launch_bounds__(kThreadsMfma) void decode_mfma_kernel(DecodeArgs a)
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       f4_t d = {0.f, 0.f, 0.f, 0.f};
-      d = mfma32(unpack_k(kw[i].x), qc[0], d);
-      d = mfma32(unpack_k(kw[i].y), qc[1], d);
-      d = mfma32(unpack_k(kw[i].z), qc[2], d);
-      d = mfma32(unpack_k(kw[i].w), qc[3], d);
+      d = mfma32(unpack_k(cb.kw[i].x), qc[0], d);
+      d = mfma32(unpack_k(cb.kw[i].y), qc[1], d);
+      d = mfma32(unpack_k(cb.kw[i].z), qc[2], d);
+      d = mfma32(unpack_k(cb.kw[i].w), qc[3], d);
       const int tb = 16 * i + 4 * kg;
-      const int4 g4 = *(const int4 *)&W.gkl[tb];
-      const uint4 s4 = *(const uint4 *)&W.s16[tb];
+      const int4 g4 = *(const int4 *)&W.gkl[sl][tb];
+      const uint4 s4 = *(const uint4 *)&W.s16[sl][tb];
       const int gr[4] = {g4.x, g4.y, g4.z, g4.w};
       const uint32_t sr[4] = {s4.x, s4.y, s4.z, s4.w};
 #pragma unroll
@@ -375,7 +391,10 @@ __global__ __launch_bounds__(kThreadsMfma) void decode_mfma_kernel(DecodeArgs a)
         const float qdotc = __builtin_fmaf(d[r], kTwo24, -s8);  // q'.c
         const float skr = (float)as_h2(sr[r]).x;
         const float s = __builtin_fmaf(skr, qdotc, qa);
-        sc[i][r] = (tb + r < nt && col < gn) ? s * kLog2e : -INFINITY;
+        // additive mask (s is finite: padding reads zeros), so that nothing
+        // above is computed under a branch
+        const float pen = (tb + r < cb.nt && col < gn) ? 0.f : -INFINITY;
+        sc[i][r] = __builtin_fmaf(s, kLog2e, pen);
         mx = fmaxf(mx, sc[i][r]);
       }
     }
@@ -398,67 +417,106 @@ __global__ __launch_bounds__(kThreadsMfma) void decode_mfma_kernel(DecodeArgs a)
     }
     const float mref = (m_run == -INFINITY) ? 0.f : m_run;  // masked heads: scores are -inf
 
-    // ---- per tile: weights, P_g, code P.V ------------------------------------------
+    // ---- weights, P_g and code P.V, two 16-token tiles per K=32 product ------------
+    // K index 8kg + e of the products below is token 16(2P) + 4kg + e (e < 4)
+    // or 16(2P+1) + 4kg + e - 4 (e >= 4): the 4 tokens the score tile gave
+    // this lane group in each of the two tiles.
     f4_t pg = {0.f, 0.f, 0.f, 0.f};  // P_g^T: lane holds groups 4kg+r, head col
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int tb = 16 * i + 4 * kg;
-      const uint4 s4 = *(const uint4 *)&W.s16[tb];
-      const int4 g4 = *(const int4 *)&W.gvl[tb];
-      // p (fp16), p*s_v and p*s_v/16 (fp16 products)
-      const h2_t p01 = h2_t{(_Float16)fast_exp2(sc[i][0] - mref), (_Float16)fast_exp2(sc[i][1] - mref)};
-      const h2_t p23 = h2_t{(_Float16)fast_exp2(sc[i][2] - mref), (_Float16)fast_exp2(sc[i][3] - mref)};
-      const h2_t sv01 = as_h2(__builtin_amdgcn_perm(s4.y, s4.x, 0x07060302u));
-      const h2_t sv23 = as_h2(__builtin_amdgcn_perm(s4.w, s4.z, 0x07060302u));
-      const h2_t w01 = p01 * sv01, w23 = p23 * sv23;
-      const h2_t x01 = w01 * sixteenth, x23 = w23 * sixteenth;
-      l_run = __builtin_amdgcn_fdot2(p01, ones, l_run, false);
-      l_run = __builtin_amdgcn_fdot2(p23, ones, l_run, false);
-      w_run = __builtin_amdgcn_fdot2(w01, ones, w_run, false);
-      w_run = __builtin_amdgcn_fdot2(w23, ones, w_run, false);
-      w16_run = __builtin_amdgcn_fdot2(x01, ones, w16_run, false);
-      w16_run = __builtin_amdgcn_fdot2(x23, ones, w16_run, false);
-      const h4_t ap = h4_t{p01.x, p01.y, p23.x, p23.y};
-      const h4_t aw = h4_t{w01.x, w01.y, w23.x, w23.y};
-      const h4_t aw16 = h4_t{x01.x, x01.y, x23.x, x23.y};
-      // E^T p^T: group (col) x tokens (4kg + r)
-      const _Float16 one = (_Float16)1.f, zero = (_Float16)0.f;
-      const h4_t e = h4_t{g4.x == col ? one : zero, g4.y == col ? one : zero,
-                          g4.z == col ? one : zero, g4.w == col ? one : zero};
-      pg = mfma16(e, ap, pg);
-      // V codes: B = 4 tokens x dim 8col + nb (nibble nb of word col)
+    for (int P = 0; P < 2; ++P) {
+      h2_t pp[2][2], ww[2][2], xx[2][2];
+      uint32_t ee[2][2];
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const int i = 2 * P + u;
+        const int tb = 16 * i + 4 * kg;
+        const uint4 s4 = *(const uint4 *)&W.s16[sl][tb];
+        const int4 g4 = *(const int4 *)&W.gvl[sl][tb];
+        // p (fp16), p*s_v and p*s_v/16 (fp16 products)
+        const h2_t p01 = h2_t{(_Float16)fast_exp2(sc[i][0] - mref), (_Float16)fast_exp2(sc[i][1] - mref)};
+        const h2_t p23 = h2_t{(_Float16)fast_exp2(sc[i][2] - mref), (_Float16)fast_exp2(sc[i][3] - mref)};
+        const h2_t sv01 = as_h2(__builtin_amdgcn_perm(s4.y, s4.x, 0x07060302u));
+        const h2_t sv23 = as_h2(__builtin_amdgcn_perm(s4.w, s4.z, 0x07060302u));
+        const h2_t w01 = p01 * sv01, w23 = p23 * sv23;
+        const h2_t x01 = w01 * sixteenth, x23 = w23 * sixteenth;
+        l_run = __builtin_amdgcn_fdot2(p01, ones, l_run, false);
+        l_run = __builtin_amdgcn_fdot2(p23, ones, l_run, false);
+        w_run = __builtin_amdgcn_fdot2(w01, ones, w_run, false);
+        w_run = __builtin_amdgcn_fdot2(w23, ones, w_run, false);
+        w16_run = __builtin_amdgcn_fdot2(x01, ones, w16_run, false);
+        w16_run = __builtin_amdgcn_fdot2(x23, ones, w16_run, false);
+        pp[u][0] = p01, pp[u][1] = p23;
+        ww[u][0] = w01, ww[u][1] = w23;
+        xx[u][0] = x01, xx[u][1] = x23;
+        // E^T: group col x these tokens (fp16 1.0 = 0x3c00)
+        ee[u][0] = (g4.x == col ? 0x3c00u : 0u) | (g4.y == col ? 0x3c000000u : 0u);
+        ee[u][1] = (g4.z == col ? 0x3c00u : 0u) | (g4.w == col ? 0x3c000000u : 0u);
+      }
+      const h8_t ap = h8_t{pp[0][0].x, pp[0][0].y, pp[0][1].x, pp[0][1].y,
+                           pp[1][0].x, pp[1][0].y, pp[1][1].x, pp[1][1].y};
+      const h8_t aw = h8_t{ww[0][0].x, ww[0][0].y, ww[0][1].x, ww[0][1].y,
+                           ww[1][0].x, ww[1][0].y, ww[1][1].x, ww[1][1].y};
+      const h8_t ax = h8_t{xx[0][0].x, xx[0][0].y, xx[0][1].x, xx[0][1].y,
+                           xx[1][0].x, xx[1][0].y, xx[1][1].x, xx[1][1].y};
+      pg = mfma32(h8_of(ee[0][0], ee[0][1], ee[1][0], ee[1][1]), ap, pg);
+      // V codes: B = 8 tokens x dim 8col + nb (nibble nb of word col)
+      const int i0 = 2 * P, i1 = 2 * P + 1;
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
         const uint32_t sel = (uint32_t)k | (0x0cu << 8) | ((uint32_t)(4 + k) << 16) | (0x0cu << 24);
-        const uint32_t q01 = __builtin_amdgcn_perm(vw[i][1], vw[i][0], sel);
-        const uint32_t q23 = __builtin_amdgcn_perm(vw[i][3], vw[i][2], sel);
-        const h4_t blo = h4_of(and_or(q01, 0x000F000Fu, magic), and_or(q23, 0x000F000Fu, magic));
-        const h4_t bhi = h4_of(and_or(q01, 0x00F000F0u, magic), and_or(q23, 0x00F000F0u, magic));
-        acc[2 * k] = mfma16(aw, blo, acc[2 * k]);
-        acc[2 * k + 1] = mfma16(aw16, bhi, acc[2 * k + 1]);
+        const uint32_t a01 = __builtin_amdgcn_perm(cb.vw[i0][1], cb.vw[i0][0], sel);
+        const uint32_t a23 = __builtin_amdgcn_perm(cb.vw[i0][3], cb.vw[i0][2], sel);
+        const uint32_t b01 = __builtin_amdgcn_perm(cb.vw[i1][1], cb.vw[i1][0], sel);
+        const uint32_t b23 = __builtin_amdgcn_perm(cb.vw[i1][3], cb.vw[i1][2], sel);
+        const h8_t blo = h8_of(and_or(a01, 0x000F000Fu, magic), and_or(a23, 0x000F000Fu, magic),
+                               and_or(b01, 0x000F000Fu, magic), and_or(b23, 0x000F000Fu, magic));
+        const h8_t bhi = h8_of(and_or(a01, 0x00F000F0u, magic), and_or(a23, 0x00F000F0u, magic),
+                               and_or(b01, 0x00F000F0u, magic), and_or(b23, 0x00F000F0u, magic));
+        acc[2 * k] = mfma32(aw, blo, acc[2 * k]);
+        acc[2 * k + 1] = mfma32(ax, bhi, acc[2 * k + 1]);
       }
     }
 
-    // ---- anchor term: P_g (hi/lo fp16) against the V anchor rows -------------------
+    // ---- anchor term: P_g as an fp16 hi/lo pair in one K=32 product ---------------
+    // K index 8kg + e: group 4kg + e, hi part (e < 4) or lo part (e >= 4); the
+    // anchor rows are duplicated in the B operand to match.
     {
       const h2_t ph01 = h2_t{(_Float16)pg[0], (_Float16)pg[1]};
       const h2_t ph23 = h2_t{(_Float16)pg[2], (_Float16)pg[3]};
       const h2_t pl01 = h2_t{(_Float16)(pg[0] - (float)ph01.x), (_Float16)(pg[1] - (float)ph01.y)};
       const h2_t pl23 = h2_t{(_Float16)(pg[2] - (float)ph23.x), (_Float16)(pg[3] - (float)ph23.y)};
-      const h4_t pa = h4_t{ph01.x, ph01.y, ph23.x, ph23.y};
-      const h4_t pl = h4_t{pl01.x, pl01.y, pl23.x, pl23.y};
+      const h8_t pa = h8_t{ph01.x, ph01.y, ph23.x, ph23.y, pl01.x, pl01.y, pl23.x, pl23.y};
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
         const h4_t blo = rows_operand(va, k, false), bhi = rows_operand(va, k, true);
-        acc[2 * k] = mfma16(pa, blo, acc[2 * k]);
-        acc[2 * k] = mfma16(pl, blo, acc[2 * k]);
-        acc[2 * k + 1] = mfma16(pa, bhi, acc[2 * k + 1]);
-        acc[2 * k + 1] = mfma16(pl, bhi, acc[2 * k + 1]);
+        acc[2 * k] = mfma32(pa, h8_t{blo[0], blo[1], blo[2], blo[3], blo[0], blo[1], blo[2], blo[3]},
+                            acc[2 * k]);
+        acc[2 * k + 1] = mfma32(pa, h8_t{bhi[0], bhi[1], bhi[2], bhi[3], bhi[0], bhi[1], bhi[2], bhi[3]},
+                                acc[2 * k + 1]);
       }
     }
-    wave_lds_sync();
-    c0l += kWaves * kChunk;
-    if (c0l < t1) stage((int)c0l);
+  };
+
+  // Software pipeline: the next chunk's loads are issued before the current
+  // chunk is computed (two register buffers, unrolled by two).
+  int64_t c0l = t0 + (int64_t)wave * kChunk;
+  if (c0l < t1) {
+    ChunkBuf bufA, bufB;
+    stage((int)c0l, bufA, 0);
+    stage_va((int)c0l);
+    prep_q();
+    for (;;) {
+      stage((int)(c0l + kWaves * kChunk), bufB, 1);
+      compute(bufA, 0);
+      c0l += kWaves * kChunk;
+      if (c0l >= t1) break;
+      stage_va((int)c0l);
+      stage((int)(c0l + kWaves * kChunk), bufA, 0);
+      compute(bufB, 1);
+      c0l += kWaves * kChunk;
+      if (c0l >= t1) break;
+      stage_va((int)c0l);
+    }
   }
 
   // ---- totals: the 4 lane groups of a column hold disjoint tokens ---------------
@@ -549,7 +607,8 @@ __global__ __launch_bounds__(kThreadsMfma) void decode_plain_kernel(DecodeArgs a
       const int tb = 16 * i + 4 * kg;
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        sc[i][r] = (tb + r < nt && col < gn) ? d[r] * kLog2e : -INFINITY;
+        const float pen = (tb + r < nt && col < gn) ? 0.f : -INFINITY;
+        sc[i][r] = __builtin_fmaf(d[r], kLog2e, pen);
         mx = fmaxf(mx, sc[i][r]);
       }
     }
@@ -567,17 +626,28 @@ __global__ __launch_bounds__(kThreadsMfma) void decode_plain_kernel(DecodeArgs a
       m_run = m_new;
     }
     const float mref = (m_run == -INFINITY) ? 0.f : m_run;
+    // P.V with two 16-token tiles per K=32 product (K index 8kg + e: token
+    // 16(2P) + 4kg + e for e < 4, 16(2P+1) + 4kg + e - 4 for e >= 4)
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const h2_t p01 = h2_t{(_Float16)fast_exp2(sc[i][0] - mref), (_Float16)fast_exp2(sc[i][1] - mref)};
-      const h2_t p23 = h2_t{(_Float16)fast_exp2(sc[i][2] - mref), (_Float16)fast_exp2(sc[i][3] - mref)};
-      l_run = __builtin_amdgcn_fdot2(p01, ones, l_run, false);
-      l_run = __builtin_amdgcn_fdot2(p23, ones, l_run, false);
-      const h4_t ap = h4_t{p01.x, p01.y, p23.x, p23.y};
+    for (int P = 0; P < 2; ++P) {
+      h2_t pp[2][2];
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const int i = 2 * P + u;
+        pp[u][0] = h2_t{(_Float16)fast_exp2(sc[i][0] - mref), (_Float16)fast_exp2(sc[i][1] - mref)};
+        pp[u][1] = h2_t{(_Float16)fast_exp2(sc[i][2] - mref), (_Float16)fast_exp2(sc[i][3] - mref)};
+        l_run = __builtin_amdgcn_fdot2(pp[u][0], ones, l_run, false);
+        l_run = __builtin_amdgcn_fdot2(pp[u][1], ones, l_run, false);
+      }
+      const h8_t ap = h8_t{pp[0][0].x, pp[0][0].y, pp[0][1].x, pp[0][1].y,
+                           pp[1][0].x, pp[1][0].y, pp[1][1].x, pp[1][1].y};
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
-        acc[2 * k] = mfma16(ap, rows_operand(vr[i], k, false), acc[2 * k]);
-        acc[2 * k + 1] = mfma16(ap, rows_operand(vr[i], k, true), acc[2 * k + 1]);
+        const h4_t l0 = rows_operand(vr[2 * P], k, false), l1 = rows_operand(vr[2 * P + 1], k, false);
+        const h4_t o0 = rows_operand(vr[2 * P], k, true), o1 = rows_operand(vr[2 * P + 1], k, true);
+        acc[2 * k] = mfma32(ap, h8_t{l0[0], l0[1], l0[2], l0[3], l1[0], l1[1], l1[2], l1[3]}, acc[2 * k]);
+        acc[2 * k + 1] =
+            mfma32(ap, h8_t{o0[0], o0[1], o0[2], o0[3], o1[0], o1[1], o1[2], o1[3]}, acc[2 * k + 1]);
       }
     }
   }
