@@ -57,6 +57,22 @@ def build_cache(cfg, dev):
     return cache, k, v, kt, vt
 
 
+def build_cache_device(cfg, dev, capacity=None):
+    """Cache filled from the on-GPU generator (workloads too large for the
+    host generator); same AR(1) statistics, different random streams."""
+    import torch
+
+    from chronoquant_mlx_amd import ChronoQuantCache, synth
+    kt, vt = synth.make_kv_device(cfg, cfg.T, cfg.B, dev)
+    cache = ChronoQuantCache(stride_k=cfg.stride_k, stride_v=cfg.stride_v,
+                             delta_bits_k=cfg.delta_bits_k, delta_bits_v=cfg.delta_bits_v,
+                             dead_zone_k=cfg.dead_zone_k, dead_zone_v=cfg.dead_zone_v,
+                             capacity=capacity or cfg.T)
+    cache.update_and_fetch(kt, vt)
+    torch.cuda.synchronize()
+    return cache, kt, vt
+
+
 def clone_cache(cache):
     import copy
     c = copy.copy(cache)
@@ -149,6 +165,126 @@ def measured_traffic(workload):
     return int(kv["traffic_bytes_per_launch"])
 
 
+def time_decode_config(name, dev, stream, steps, warmup, timer, device_gen):
+    """Fused decode of one configuration (full context, every sequence at T):
+    us/layer and algorithmic GB/s over cycled cache replicas."""
+    import torch
+
+    from chronoquant_mlx_amd import _lib, synth
+    cfg = synth.CONFIGS[name]
+    if device_gen:
+        cache, kt, vt = build_cache_device(cfg, dev)
+    else:
+        cache, _, _, kt, vt = build_cache(cfg, dev)
+    del kt, vt
+    q = torch.randn(cfg.B, cfg.n_q_heads, cfg.head_dim, device=dev).half()
+    scale = cfg.head_dim ** -0.5
+    algo = synth.algorithmic_decode_bytes(cfg)
+    reps = max(2, int(np.ceil(2.2 * MALL_BYTES / cache.nbytes)))
+    caches = [cache] + [clone_cache(cache) for _ in range(reps - 1)]
+    out = torch.empty(cfg.B, cfg.n_q_heads, cfg.head_dim, dtype=torch.float16, device=dev)
+    L = _lib.load()
+    ws = caches[0]._decode_workspace(cfg.n_q_heads)
+    descs = [c._descriptor() for c in caches]
+
+    def mk(desc):
+        def f():
+            st = L.cq_decode_attn(desc, q.data_ptr(), _lib.CQ_F16, cfg.n_q_heads, scale, None,
+                                  cfg.T, cfg.T, out.data_ptr(), _lib.CQ_F16, ws.data_ptr(),
+                                  ws.numel(), torch.cuda.current_stream().cuda_stream)
+            assert st == 0, _lib.status_string(st)
+        return f
+
+    ms = timer([mk(d) for d in descs], steps, warmup, stream)
+    gbs = algo / (ms * 1e-3) / 1e9
+    log(f"[bench] {name}: {ms * 1e3:.2f} us/layer, {gbs:.0f} GB/s")
+    res = {"workload": f"B={cfg.B} GQA {cfg.n_q_heads}q/{cfg.n_kv_heads}kv T={cfg.T} strides "
+                       f"{cfg.stride_k}/{cfg.stride_v} bits {cfg.delta_bits_k}/{cfg.delta_bits_v} "
+                       f"dz {cfg.dead_zone_k}/{cfg.dead_zone_v}",
+           "us_per_layer": round(ms * 1e3, 3), "GBps": round(gbs, 1),
+           "frac": round(gbs / HBM_PEAK_GBS, 4), "algorithmic_bytes_per_step": algo,
+           "replicas": reps, "data": "on-GPU AR(1) generator" if device_gen else "seeded AR(1)"}
+    del caches, cache
+    torch.cuda.empty_cache()
+    return res
+
+
+def time_streaming(name, dev, stream, n_steps=256):
+    """a ragged batch, each step appends one token per sequence
+    (I-frame every stride, else quantise + pack against the anchor) and runs
+    the fused decode over the per-sequence lengths; the n_steps steps are one
+    HIP graph, timed once after an untimed replay."""
+    import torch
+
+    from chronoquant_mlx_amd import _lib, synth
+    cfg = synth.CONFIGS[name]
+    B, H, D, nq = cfg.B, cfg.n_kv_heads, cfg.head_dim, cfg.n_q_heads
+    lens = cfg.lengths()
+    t_max = int(lens.max())
+    cap = t_max + n_steps
+    import dataclasses
+    gcfg = dataclasses.replace(cfg, T=cap)
+    cache, kt, vt = build_cache_device(gcfg, dev, capacity=cap)
+    # every sequence holds t_max tokens; sequence b continues at lens[b]
+    L = _lib.load()
+    desc = cache._descriptor()
+    off0 = torch.tensor(lens, dtype=torch.int32, device=dev)
+    off = off0.clone()
+    off1 = off0 + 1
+    q = torch.randn(B, nq, D, device=dev).half()
+    out = torch.empty(B, nq, D, dtype=torch.float16, device=dev)
+    need = L.cq_decode_workspace_size(B, H, nq, D, cap)
+    ws = torch.zeros(need, dtype=torch.uint8, device=dev)
+    ks = (ctypes.c_int64 * 3)(*kt.stride()[:3])
+    vs = (ctypes.c_int64 * 3)(*vt.stride()[:3])
+    scale = D ** -0.5
+
+    def step(s):
+        sp = torch.cuda.current_stream().cuda_stream
+        kn, vn = kt[:, :, t_max + s - n_steps], vt[:, :, t_max + s - n_steps]
+        st = L.cq_append(desc, kn.data_ptr(), ks, vn.data_ptr(), vs, _lib.CQ_F16, 1,
+                         off.data_ptr(), 0, sp)
+        assert st == 0, _lib.status_string(st)
+        st = L.cq_decode_attn(desc, q.data_ptr(), _lib.CQ_F16, nq, scale, off1.data_ptr(), 0, cap,
+                              out.data_ptr(), _lib.CQ_F16, ws.data_ptr(), need, sp)
+        assert st == 0, _lib.status_string(st)
+        off.add_(1)
+        off1.add_(1)
+
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=stream):
+        for s in range(n_steps):
+            step(s)
+    def reset():
+        off.copy_(off0)
+        off1.copy_(off0 + 1)
+        torch.cuda.synchronize()
+    reset()
+    g.replay()
+    reset()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    with torch.cuda.stream(stream):
+        e0.record(stream)
+        g.replay()
+        e1.record(stream)
+    e1.synchronize()
+    ms = e0.elapsed_time(e1) / n_steps
+    algo = int(np.mean([synth.algorithmic_decode_bytes(cfg, lens + s + 1) for s in range(n_steps)]))
+    gbs = algo / (ms * 1e-3) / 1e9
+    log(f"[bench] {name}: {ms * 1e3:.2f} us/step (append + decode), {gbs:.0f} GB/s")
+    res = {"workload": f"B={B} ragged T_b~U[{cfg.ragged_min},{cfg.T}] GQA {nq}q/{H}kv strides "
+                       f"{cfg.stride_k}/{cfg.stride_v}; {n_steps} steps of append(1 token/seq) + "
+                       f"fused decode, one HIP graph",
+           "us_per_step": round(ms * 1e3, 3), "GBps": round(gbs, 1),
+           "frac": round(gbs / HBM_PEAK_GBS, 4), "algorithmic_bytes_per_step": algo,
+           "data": "on-GPU AR(1) generator"}
+    del g, cache, kt, vt
+    torch.cuda.empty_cache()
+    return res
+
+
 def cpu_baseline(cfg, k, v, q, budget_s=12.0):
     from oracle import oracle as O
     threads = min(16, len(os.sched_getaffinity(0)))
@@ -182,6 +318,8 @@ def main():
                     help="launch without a HIP graph (for rocprofv3 --pmc passes)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run plain 256 MiB copies (counter scale reference)")
+    ap.add_argument("--no-extra", action="store_true",
+                    help="skip the supplementary ftv3_16k / c2 / c3 measurements")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on exactly one GPU; --gpus must be 1 "
@@ -279,6 +417,18 @@ def main():
         result["fp16_baseline"] = {"us_per_layer": round(ms16 * 1e3, 3),
                                    "GBps": round(fp16_bytes / (ms16 * 1e-3) / 1e9, 1),
                                    "speedup_of_compressed": round(ms16 / ms, 3)}
+
+    if not args.no_extra:
+        extra = {}
+        extra["ftv3_16k"] = time_decode_config("ftv3_16k", dev, stream, args.steps, args.warmup,
+                                               timer, device_gen=False)
+        if "fp16_baseline" in result:  # same K/V shape as the main workload
+            extra["ftv3_16k"]["speedup_vs_fp16"] = round(
+                result["fp16_baseline"]["us_per_layer"] / extra["ftv3_16k"]["us_per_layer"], 3)
+        extra["c2"] = time_decode_config("c2", dev, stream, max(20, args.steps // 4),
+                                         args.warmup, timer, device_gen=True)
+        extra["c3"] = time_streaming("c3", dev, stream)
+        result["extra"] = extra
 
     if not args.no_cpu_baseline:
         log("[bench] CPU baseline (oracle restatement of reconstruct + fallback SDPA)")

@@ -54,6 +54,11 @@ CONFIGS = {
                        dead_zone_k=0.0, dead_zone_v=0.05, outlier_frac=0.01),
     "c3": DecodeConfig("c3", B=32, n_q_heads=32, n_kv_heads=8, head_dim=128, T=32768,
                        stride_k=32, stride_v=8, dead_zone_v=0.05, ragged_min=1024),
+    # the north star's target shape: configs[1]'s GQA 32/8 @16K with Full-Throttle V3
+    "ftv3_16k": DecodeConfig("ftv3_16k", B=1, n_q_heads=32, n_kv_heads=8, head_dim=128,
+                             T=16384, stride_k=64, stride_v=32, delta_bits_k=4,
+                             delta_bits_v=3, dead_zone_k=0.0, dead_zone_v=0.05,
+                             outlier_frac=0.01),
 }
 
 
@@ -117,3 +122,40 @@ def algorithmic_decode_bytes(cfg: DecodeConfig, lengths=None) -> int:
     cache = sum(compressed_bytes(int(T), cfg.n_kv_heads, cfg.head_dim, cfg.stride_k,
                                  cfg.stride_v) for T in lengths)
     return cache + 2 * len(lengths) * cfg.n_q_heads * cfg.head_dim * 2
+
+
+def make_kv_device(cfg: DecodeConfig, T: int, B: int, device, seed: int = 7000):
+    """(K, V) fp16 [B, H, T, D] with the same AR(1) statistics, generated on
+    the GPU (torch Philox) for workloads too large for the host generator.
+    The recurrence is evaluated in 256-token chunks in closed form:
+    x_{t+i} = rho^(i+1) x_{t-1} + sum_{j<=i} rho^(i-j) e_j."""
+    import torch
+    H, D = cfg.n_kv_heads, cfg.head_dim
+    rho, noise, L = cfg.rho, cfg.noise, 256
+    j = torch.arange(L, device=device, dtype=torch.float64)
+    pw = (rho ** (j + 1)).float()[:, None]
+    fwd = (rho ** j).float()[:, None]
+    inv = (rho ** (-j)).float()[:, None]
+    outs = []
+    for comp in range(2):
+        g = torch.Generator(device=device)
+        g.manual_seed(seed + comp)
+        sig = torch.exp(0.5 * torch.randn(B, H, D, generator=g, device=device))
+        n_out = int(round(cfg.outlier_frac * H * D))
+        if n_out:
+            for b in range(B):
+                idx = torch.randperm(H * D, generator=g, device=device)[:n_out]
+                sig[b].view(-1)[idx] *= 8.0
+        out = torch.empty(B, H, T, D, dtype=torch.float16, device=device)
+        x = torch.randn(B, H, 1, D, generator=g, device=device) * (noise / (1.0 - rho * rho) ** 0.5)
+        out[:, :, :1] = (sig[:, :, None, :] * x).half()
+        t = 1
+        while t < T:
+            n = min(L, T - t)
+            eps = torch.randn(B, H, n, D, generator=g, device=device) * noise
+            xs = pw[:n] * x + fwd[:n] * torch.cumsum(eps * inv[:n], dim=2)
+            out[:, :, t:t + n] = (sig[:, :, None, :] * xs).half()
+            x = xs[:, :, n - 1:n]
+            t += n
+        outs.append(out)
+    return outs[0], outs[1]
