@@ -425,8 +425,8 @@ def main():
         if "fp16_baseline" in result:  # same K/V shape as the main workload
             extra["ftv3_16k"]["speedup_vs_fp16"] = round(
                 result["fp16_baseline"]["us_per_layer"] / extra["ftv3_16k"]["us_per_layer"], 3)
-        extra["c2"] = time_decode_config("c2", dev, stream, max(20, args.steps // 4),
-                                         args.warmup, timer, device_gen=True)
+        extra["c2"] = time_decode_config("c2", dev, stream, args.steps, args.warmup, timer,
+                                         device_gen=True)
         extra["c3"] = time_streaming("c3", dev, stream)
         result["extra"] = extra
 

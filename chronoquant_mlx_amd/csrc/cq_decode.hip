@@ -6,6 +6,9 @@
 // once per chunk.  cq_decode_attn routes head_dim 128 with fp16 queries to the
 // MFMA kernel (cq_decode_mfma.hip) and everything else to the portable kernel.
 #include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <atomic>
 #include <math.h>
 
 #include "cq_decode_common.h"
@@ -207,8 +210,37 @@ static int lpt_log2_for(int W) {
   return l;
 }
 
+int64_t resident_workgroups(const void *kernel, int threads, int slot) {
+  constexpr int kMaxDevices = 64;
+  static std::atomic<int64_t> cache[kMaxDevices][kSlotCount];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) dev = 0;
+  const bool cached = dev >= 0 && dev < kMaxDevices;
+  if (cached) {
+    const int64_t v = cache[dev][slot].load(std::memory_order_relaxed);
+    if (v > 0) return v;
+  }
+  int cus = 0, per_cu = 0;
+  const bool ok =
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess &&
+      hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, threads, 0) == hipSuccess &&
+      cus > 0 && per_cu > 0;
+  (void)hipGetLastError();
+  if (!ok) return 256;  // no device answer: plan for one MI355X generation
+  const int64_t v = (int64_t)cus * per_cu;
+  if (cached) cache[dev][slot].store(v, std::memory_order_relaxed);
+  return v;
+}
+
+static int64_t generic_resident() {
+  return resident_workgroups(reinterpret_cast<const void *>(decode_generic_kernel), 256,
+                             kSlotGeneric);
+}
+
+int64_t decode_max_resident() { return std::max(generic_resident(), mfma_max_resident()); }
+
 static int launch_generic(DecodeArgs &a, void *workspace, size_t ws_bytes, hipStream_t stream) {
-  int st = prepare_launch(a, kGenericGroup, workspace, ws_bytes);
+  int st = prepare_launch(a, kGenericGroup, generic_resident(), workspace, ws_bytes);
   if (st) return st;
   a.lpt_log2 = lpt_log2_for(a.W);
   const dim3 grid((unsigned)a.nsplit, (unsigned)(a.H * a.n_chunks), (unsigned)a.B);
@@ -279,7 +311,7 @@ extern "C" {
 size_t cq_decode_workspace_size(int32_t batch, int32_t n_kv_heads, int32_t n_q_heads,
                                 int32_t head_dim, int64_t max_seq_len) {
   if (batch < 1 || n_kv_heads < 1 || n_q_heads < 1 || head_dim < 1) return 0;
-  const SplitPlan p = plan_splits(batch, n_kv_heads, max_seq_len);
+  const SplitPlan p = plan_splits((int64_t)batch * n_kv_heads, max_seq_len, decode_max_resident());
   return workspace_bytes_for(batch, n_q_heads, head_dim, p.nsplit);
 }
 

@@ -258,13 +258,22 @@ struct SplitPlan {
   int64_t split_len;
 };
 
-// Splits of kSplitGranule-multiple length, sized so that the grid holds about
-// two workgroups per CU (256 CUs) when the context allows, at most kMaxSplits.
-inline SplitPlan plan_splits(int B, int H, int64_t max_T) {
+// Workgroups of `kernel` (launched with `threads` threads) that run at once on
+// the current device: CUs x maximum active blocks per CU, cached per device
+// under `slot` (one slot per decode kernel).
+enum ResidentSlot { kSlotGeneric = 0, kSlotMfmaPow2, kSlotMfma, kSlotPlain, kSlotCount };
+int64_t resident_workgroups(const void *kernel, int threads, int slot);
+int64_t mfma_max_resident();     // max over the MFMA-file kernels
+int64_t decode_max_resident();   // max over every decode kernel
+
+// Splits of kSplitGranule-multiple length sized so that the whole grid
+// (groups workgroups per split) is resident at once: one generation of
+// workgroups, no tail of late starters.  At most kMaxSplits.
+inline SplitPlan plan_splits(int64_t groups, int64_t max_T, int64_t target) {
   SplitPlan p;
-  const int64_t groups = (int64_t)B * H;
-  const int64_t target = 512;
-  int64_t ns = (target + groups - 1) / groups;
+  if (groups < 1) groups = 1;
+  if (target < 1) target = 1;
+  int64_t ns = max((int64_t)1, target / groups);
   if (max_T <= 0) max_T = 1;
   int64_t len = (max_T + ns - 1) / ns;
   len = (len + kSplitGranule - 1) / kSplitGranule * kSplitGranule;
@@ -306,11 +315,15 @@ inline void carve_workspace(DecodeArgs &a, void *ws) {
 }
 
 // Common launch preparation: split plan and workspace.  chunk_heads = q heads
-// per workgroup of the kernel being launched.
-inline int prepare_launch(DecodeArgs &a, int chunk_heads, void *workspace, size_t ws_bytes) {
+// per workgroup of the kernel being launched; resident = its resident
+// workgroup capacity.  The plan never has more splits than the one
+// cq_decode_workspace_size sizes for (fewer groups per split there, and the
+// largest capacity of any decode kernel).
+inline int prepare_launch(DecodeArgs &a, int chunk_heads, int64_t resident, void *workspace,
+                          size_t ws_bytes) {
   a.chunk_heads = chunk_heads;
   a.n_chunks = (a.G + chunk_heads - 1) / chunk_heads;
-  const SplitPlan p = plan_splits(a.B, a.H, a.max_T);
+  const SplitPlan p = plan_splits((int64_t)a.B * a.H * a.n_chunks, a.max_T, resident);
   a.nsplit = p.nsplit;
   a.split_len = p.split_len;
   if (a.nsplit > 1) {

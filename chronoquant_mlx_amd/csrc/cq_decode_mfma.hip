@@ -35,6 +35,8 @@
 #include <hip/hip_runtime.h>
 #include <math.h>
 
+#include <algorithm>
+
 #include "cq_decode_common.h"
 
 namespace cq {
@@ -227,6 +229,9 @@ __device__ __forceinline__ void merge_and_finish(const DecodeArgs &a, DecodeLds 
 // ---------------------------------------------------------------------------
 // compressed cache
 // ---------------------------------------------------------------------------
+// Pow2: both strides are powers of two, so token -> anchor / slot arithmetic
+// is shifts and masks instead of the float-reciprocal division.
+template <bool Pow2>
 __global__ __launch_bounds__(kThreadsMfma) void decode_mfma_kernel(DecodeArgs a) {
   __shared__ DecodeLds lds;
   const int split = blockIdx.x;
@@ -244,6 +249,9 @@ __global__ __launch_bounds__(kThreadsMfma) void decode_mfma_kernel(DecodeArgs a)
   const int64_t t1 = min(T, t0 + a.split_len);
   const int sk = a.stride[0], sv = a.stride[1];
   const float isk = a.inv_stride[0], isv = a.inv_stride[1];
+  const int lsk = Pow2 ? __builtin_ctz(sk) : 0, lsv = Pow2 ? __builtin_ctz(sv) : 0;
+  auto div_k = [&](int t) { return Pow2 ? t >> lsk : div_stride(t, sk, isk); };
+  auto div_v = [&](int t) { return Pow2 ? t >> lsv : div_stride(t, sv, isv); };
 
   const __amdgpu_buffer_rsrc_t r_kfk =
       make_rsrc(a.kf[0] + bh * a.cap_kf[0] * kD, (uint32_t)(a.cap_kf[0] * kD * 2));
@@ -286,9 +294,9 @@ __global__ __launch_bounds__(kThreadsMfma) void decode_mfma_kernel(DecodeArgs a)
   auto stage = [&](int c0, ChunkBuf &cb, int sl) {
     const int nt = (int)max((int64_t)0, min((int64_t)kChunk, t1 - c0));
     cb.nt = nt;
-    const int gk_base = div_stride(c0, sk, isk);
-    const int gk_last = nt ? div_stride(c0 + nt - 1, sk, isk) : gk_base;
-    const int gv_base = div_stride(c0, sv, isv);
+    const int gk_base = div_k(c0);
+    const int gk_last = nt ? div_k(c0 + nt - 1) : gk_base;
+    const int gv_base = div_v(c0);
     // anchor offsets stay below 2^30; buffers are below 2^31 bytes (mfma_supported)
     const uint32_t dead = nt ? 0u : 0x80000000u;
     // token phase: one token per lane; scale loads first
@@ -296,7 +304,7 @@ __global__ __launch_bounds__(kThreadsMfma) void decode_mfma_kernel(DecodeArgs a)
     {
       const bool valid = lane < nt;
       const int t = c0 + (valid ? lane : max(nt - 1, 0));
-      const int gk = div_stride(t, sk, isk), gv = div_stride(t, sv, isv);
+      const int gk = div_k(t), gv = div_v(t);
       const int slk = (valid && t != gk * sk) ? t - gk - 1 : -1;
       const int slv = (valid && t != gv * sv) ? t - gv - 1 : -1;
       // slot -1 reads past the buffer: 0 (no scale)
@@ -333,8 +341,8 @@ __global__ __launch_bounds__(kThreadsMfma) void decode_mfma_kernel(DecodeArgs a)
   uint4 va[4];
   auto stage_va = [&](int c0) {
     const int nt = (int)max((int64_t)0, min((int64_t)kChunk, t1 - c0));
-    const int gv_base = div_stride(c0, sv, isv);
-    const int gv_last = nt ? div_stride(c0 + nt - 1, sv, isv) : gv_base;
+    const int gv_base = div_v(c0);
+    const int gv_last = nt ? div_v(c0 + nt - 1) : gv_base;
     const uint32_t dead = nt ? 0u : 0x80000000u;
 #pragma unroll
     for (int r = 0; r < 4; ++r)
@@ -390,14 +398,22 @@ __global__ __launch_bounds__(kThreadsMfma) void decode_mfma_kernel(DecodeArgs a)
         const float qa = W.qa[gr[r]][col];
         const float qdotc = __builtin_fmaf(d[r], kTwo24, -s8);  // q'.c
         const float skr = (float)as_h2(sr[r]).x;
-        const float s = __builtin_fmaf(skr, qdotc, qa);
-        // additive mask (s is finite: padding reads zeros), so that nothing
-        // above is computed under a branch
-        const float pen = (tb + r < cb.nt && col < gn) ? 0.f : -INFINITY;
-        sc[i][r] = __builtin_fmaf(s, kLog2e, pen);
-        mx = fmaxf(mx, sc[i][r]);
+        sc[i][r] = __builtin_fmaf(skr, qdotc, qa) * kLog2e;
       }
     }
+    // Tokens past the end exist only in a split's last chunk (a uniform
+    // branch).  Columns of q heads >= gn are not masked: their q' is zero,
+    // their scores finite, and their rows of acc / l are never read.
+    if (cb.nt < kChunk) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          if (16 * i + 4 * kg + r >= cb.nt) sc[i][r] = -INFINITY;
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      mx = fmaxf(mx, fmaxf(fmaxf(sc[i][0], sc[i][1]), fmaxf(sc[i][2], sc[i][3])));
 
     // ---- lazy running max for the chunk ------------------------------------------
     mx = shfl_max_kg(mx);
@@ -675,14 +691,29 @@ bool mfma_supported(const DecodeArgs &a) {
   return (al & 15u) == 0;
 }
 
+static int64_t resident_of(int slot) {
+  const void *k = slot == kSlotPlain ? reinterpret_cast<const void *>(decode_plain_kernel)
+                  : slot == kSlotMfmaPow2 ? reinterpret_cast<const void *>(decode_mfma_kernel<true>)
+                                          : reinterpret_cast<const void *>(decode_mfma_kernel<false>);
+  return resident_workgroups(k, kThreadsMfma, slot);
+}
+
+int64_t mfma_max_resident() {
+  return std::max(resident_of(kSlotPlain), std::max(resident_of(kSlotMfmaPow2), resident_of(kSlotMfma)));
+}
+
 int launch_decode_mfma(DecodeArgs &a, void *workspace, size_t ws_bytes, hipStream_t stream) {
-  int st = prepare_launch(a, kHeads, workspace, ws_bytes);
+  const bool pow2 = ((a.stride[0] & (a.stride[0] - 1)) | (a.stride[1] & (a.stride[1] - 1))) == 0;
+  const int slot = plain_mode(a) ? kSlotPlain : pow2 ? kSlotMfmaPow2 : kSlotMfma;
+  int st = prepare_launch(a, kHeads, resident_of(slot), workspace, ws_bytes);
   if (st) return st;
   const dim3 grid((unsigned)a.nsplit, (unsigned)(a.H * a.n_chunks), (unsigned)a.B);
-  if (plain_mode(a))
+  if (slot == kSlotPlain)
     decode_plain_kernel<<<grid, dim3(kThreadsMfma), 0, stream>>>(a);
+  else if (slot == kSlotMfmaPow2)
+    decode_mfma_kernel<true><<<grid, dim3(kThreadsMfma), 0, stream>>>(a);
   else
-    decode_mfma_kernel<<<grid, dim3(kThreadsMfma), 0, stream>>>(a);
+    decode_mfma_kernel<false><<<grid, dim3(kThreadsMfma), 0, stream>>>(a);
   return hipGetLastError() == hipSuccess ? CQ_OK : CQ_ERR_LAUNCH;
 }
 

@@ -88,6 +88,26 @@ def test_shapes(G, H, D):
                          mfma=not generic)
 
 
+@pytest.mark.parametrize("sk,sv", [(5, 6), (12, 20), (48, 7), (4, 96), (33, 4)])
+def test_strides_not_powers_of_two(sk, sv):
+    # the MFMA kernel's float-reciprocal token -> anchor / slot path (power-of
+    # two strides take shifts), including strides that do not divide the
+    # 64-token chunk and groups that straddle chunks and splits
+    rng = np.random.default_rng(sk * 100 + sv)
+    B, H, T, D, G = 2, 2, 1500, 128, 4
+    k = np.cumsum(rng.standard_normal((B, H, T, D)) * 0.1, axis=2).astype(np.float16)
+    v = np.cumsum(rng.standard_normal((B, H, T, D)) * 0.1, axis=2).astype(np.float16)
+    q = rng.standard_normal((B, G * H, D)).astype(np.float16)
+    params = dict(stride_k=sk, stride_v=sv)
+    cache = build_gpu_cache(k, v, **params)
+    scale = D ** -0.5
+    out = decode_gpu(cache, q, scale)
+    for b in range(B):
+        ck, cv = build_oracle(k[b], v[b], **params)
+        assert_close(out[b], oracle_fallback(ck, cv, q[b], scale), what=f"b={b}")
+        assert_tight(out[b], O.sdpa_fused(q[b], ck, cv, scale), what=f"b={b}")
+
+
 def test_workspace_shared_across_shapes():
     # regression: calls with different split counts share the per-device
     # workspace; counters must stay valid between them
