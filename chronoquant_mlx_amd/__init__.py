@@ -14,6 +14,7 @@ from .patch import (
     revert,
 )
 from .attention import chronoquant_sdpa
+from .persist import load_prompt_cache, save_prompt_cache
 
 __all__ = [
     "ChronoQuantCache",
@@ -24,4 +25,7 @@ __all__ = [
     "create_full_throttle_caches",
     "chronoquant_sdpa",
     "revert",
+    # prompt-cache files (mlx_lm's save_prompt_cache / load_prompt_cache)
+    "save_prompt_cache",
+    "load_prompt_cache",
 ]

@@ -339,7 +339,14 @@ class ChronoQuantCache:
         if len(values) >= 6:
             pk_k, sc_k, pk_v, sc_v = values[2], values[3], values[4], values[5]
         elif len(values) >= 4:
-            pk_k, sc_k = values[2], values[3]
+            # The reference emits a component's packed/scales pair only when
+            # it has P-frames (cache.py:227-231) but reads a lone pair as the
+            # keys' (cache.py:243-246).  With stride_k == 1 the keys never
+            # have P-frames, so a lone pair can only be the values'.
+            if self.stride_k == 1 and self.stride_v > 1:
+                pk_v, sc_v = values[2], values[3]
+            else:
+                pk_k, sc_k = values[2], values[3]
         B, H, _, D = kf_k.shape
         self.head_dim = D
         self._shape = (B, H, D)
