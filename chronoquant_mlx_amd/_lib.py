@@ -74,6 +74,7 @@ SIGNATURES = {
     "cq_decode_attn_generic": ([_DESC, _P, _I32, _I32, _F, _P, _I64, _I64, _P, _I32, _P, _SZ, _P], _I32),
     "cq_fp16_decode_attn": ([_P, _P, _I64, _I32, _I32, _I32, _P, _I32, _I32, _F, _P, _I64, _I64,
                              _P, _I32, _P, _SZ, _P], _I32),
+    "cq_prefill_attn": ([_DESC, _P, _I32, _I32, _I64, _F, _I32, _I64, _P, _P], _I32),
     "cq_status_string": ([_I32], ctypes.c_char_p),
 }
 

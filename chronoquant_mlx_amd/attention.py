@@ -5,16 +5,26 @@ the gfx950 split-K decode kernel (cq_decode_attn).  The reference takes it
 only for B == 1 (its Metal kernel has no batch axis); the gfx950 kernel has
 one, so any batch size with q_len == 1 takes it here.
 
-Fallback (q_len > 1, array masks, use_fused=False): reconstruct fp16 K/V on
-the GPU (cq_reconstruct) and run dense GQA attention with the reference's
-rounding points: q' = fp16(q * fp16(scale)), fp16 scores, mask, softmax in
-fp32 rounded to the query dtype, fp16 weights @ V.
+Prefill (q_len > 1, mask None or "causal", head_dim 128, fp16): the gfx950
+chunked-prefill kernel (cq_prefill_attn), which computes the fallback's
+semantics from the compressed cache without materialising K/V.
+
+Fallback (array masks, other shapes): reconstruct fp16 K/V on the GPU
+(cq_reconstruct) and run dense GQA attention with the reference's rounding
+points: q' = fp16(q * fp16(scale)), fp16 scores, mask, softmax in fp32
+rounded to the query dtype, fp16 weights @ V.
 """
 from __future__ import annotations
 
 import torch
 
-from .kernels import MAX_FUSED_HEAD_DIM, chronoquant_sdpa_kernel
+from .kernels import (MAX_FUSED_HEAD_DIM, chronoquant_prefill_kernel, chronoquant_sdpa_kernel,
+                      prefill_supported)
+
+# q_len > 1 with mask None / "causal" runs the gfx950 chunked-prefill kernel
+# (same semantics as the reconstruct fallback below); False forces the
+# fallback, which the tests use as a second implementation.
+PREFILL_KERNEL = True
 
 
 def _apply_mask(scores: torch.Tensor, mask):
@@ -50,6 +60,9 @@ def chronoquant_sdpa(queries: torch.Tensor, keys, values, cache, scale: float, m
         q = queries.reshape(batch, n_q_heads, head_dim)
         out = chronoquant_sdpa_kernel(q, cache, scale)
         return out.reshape(batch, n_q_heads, q_len, head_dim)
+
+    if PREFILL_KERNEL and prefill_supported(queries, cache, mask):
+        return chronoquant_prefill_kernel(queries, cache, scale, causal=mask is not None)
 
     full_k, full_v = cache.reconstruct_history()
     n_kv_heads = full_k.shape[1]

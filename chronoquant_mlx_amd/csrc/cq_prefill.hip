@@ -1,0 +1,346 @@
+// cq_prefill.hip — gfx950 chunked-prefill attention over the ChronoQuant cache
+// (head_dim 128, fp16 queries): the last n_q cached tokens of every sequence
+// attend to the cache, causally or to all of it.
+//
+// Reference semantics: the reconstruct fallback of chronoquant_sdpa for
+// q_len > 1 (attention.py:61-74 over cache.py:131-160): K and V rebuilt in
+// fp16 as r = fp16(a + fp16(fp16(c) * s)), q' = fp16(q * fp16(scale)),
+// scores rounded to fp16, causal mask q_idx >= k_idx (attention.py:12-16),
+// softmax in fp32, fp16 weights against V, fp16 output.  Here the softmax is
+// the online (flash) form, with the weights rounded to fp16 where they enter
+// the P.V product.
+//
+// Workgroup = 4 waves = 64 query rows of one kv head: 64 / G positions x the
+// G q heads of the group (row R: position p0 + R / G, head R % G).  Per
+// 64-key block:
+//   1. all 256 threads rebuild the K block (row-major) and the V block
+//      (transposed, dims x keys) in LDS with the reference's fp16 rounding;
+//   2. each wave computes S^T = K . Q^T for its 16 rows (v_mfma_f32_16x16x32_f16,
+//      4 key tiles x 4 K-steps), so a lane holds 16 scores of one row;
+//   3. online softmax in the log2 domain (lazy rescale beyond 2^8);
+//   4. O += P . V (8 dim tiles x 2 K-steps; two 16-key tiles per K=32 step).
+// Inside each 8-dim group the LDS blocks and the Q fragment use the dim order
+// {0,2,4,6,1,3,5,7}, the order the nibble unpack produces; the output store
+// undoes it.
+#include <hip/hip_runtime.h>
+#include <math.h>
+
+#include "cq_decode_common.h"
+
+namespace cq {
+namespace {
+
+typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 h4_t __attribute__((ext_vector_type(4)));
+typedef _Float16 h8_t __attribute__((ext_vector_type(8)));
+typedef float f4_t __attribute__((ext_vector_type(4)));
+typedef int i4_t __attribute__((ext_vector_type(4)));
+
+constexpr int kD = 128;
+constexpr int kRows = 64;        // query rows per workgroup
+constexpr int kKeys = 64;        // keys per block
+constexpr int kThreads = 256;    // 4 waves
+constexpr int kKStride = kD + 8;      // K block row stride (fp16 elements)
+constexpr int kVStride = kKeys + 8;   // V^T block row stride (fp16 elements)
+constexpr float kTau = 8.f;
+
+struct PrefillArgs {
+  const uint16_t *kf[2];
+  const uint32_t *pk[2];
+  const uint16_t *sc[2];
+  int64_t cap_kf[2], cap_pf[2];
+  int stride[2];
+  float inv_stride[2];
+  int B, H, G, nq;
+  int64_t n_q, T;
+  int causal;
+  float scale;
+  const uint16_t *q;  // [B][nq][n_q][D] fp16
+  uint16_t *out;      // [B][nq][n_q][D] fp16
+};
+
+__device__ __forceinline__ h2_t as_h2(uint32_t u) { return __builtin_bit_cast(h2_t, u); }
+__device__ __forceinline__ uint32_t as_u(h2_t h) { return __builtin_bit_cast(uint32_t, h); }
+__device__ __forceinline__ h8_t h8_of(uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
+  const h2_t x = as_h2(a), y = as_h2(b), z = as_h2(c), w = as_h2(d);
+  return h8_t{x.x, x.y, y.x, y.y, z.x, z.y, w.x, w.y};
+}
+__device__ __forceinline__ f4_t mfma32(h8_t a, h8_t b, f4_t c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ uint4 bload128(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  const i4_t v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0);
+  return uint4{(uint32_t)v[0], (uint32_t)v[1], (uint32_t)v[2], (uint32_t)v[3]};
+}
+__device__ __forceinline__ uint32_t bload32(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(r, (int)off, 0, 0);
+}
+__device__ __forceinline__ uint32_t bload16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(r, (int)off, 0, 0);
+}
+
+// One code word (8 nibbles, dims 0..7 of a group) and the group's fp16
+// anchor (a01, a23, a45, a67) -> the rebuilt fp16 values as pairs
+// (0,2) (4,6) (1,3) (5,7): fp16(a + fp16(fp16(n - 8) * s)).  A nibble becomes
+// fp16 1024 + n by a byte permute against the magic constant; subtracting
+// 1032 is exact.  Codes past the end of the cache read as 0 and the scale as
+// 0, so c * s = -0 and an I-frame row is its anchor exactly.
+__device__ __forceinline__ uint4 rebuild8(uint32_t cw, uint4 a, h2_t s2, uint32_t magic) {
+  const uint32_t lo = cw & 0x0F0F0F0Fu, hi = (cw >> 4) & 0x0F0F0F0Fu;
+  const h2_t bias = {(_Float16)-1032.f, (_Float16)-1032.f};
+  const uint32_t sel_a = 0x07010500u, sel_b = 0x07030502u;  // bytes (0,1) / (2,3) of the nibbles
+  const h2_t c02 = as_h2(__builtin_amdgcn_perm(magic, lo, sel_a)) + bias;
+  const h2_t c46 = as_h2(__builtin_amdgcn_perm(magic, lo, sel_b)) + bias;
+  const h2_t c13 = as_h2(__builtin_amdgcn_perm(magic, hi, sel_a)) + bias;
+  const h2_t c57 = as_h2(__builtin_amdgcn_perm(magic, hi, sel_b)) + bias;
+  const h2_t a02 = as_h2(__builtin_amdgcn_perm(a.y, a.x, 0x05040100u));
+  const h2_t a46 = as_h2(__builtin_amdgcn_perm(a.w, a.z, 0x05040100u));
+  const h2_t a13 = as_h2(__builtin_amdgcn_perm(a.y, a.x, 0x07060302u));
+  const h2_t a57 = as_h2(__builtin_amdgcn_perm(a.w, a.z, 0x07060302u));
+  return uint4{as_u(a02 + c02 * s2), as_u(a46 + c46 * s2), as_u(a13 + c13 * s2),
+               as_u(a57 + c57 * s2)};
+}
+
+struct alignas(16) PrefillLds {
+  uint16_t k[kKeys][kKStride];  // K block, [key][dim (grouped order)]
+  uint16_t v[kD][kVStride];     // V block transposed, [dim (grouped order)][key]
+};
+
+__global__ __launch_bounds__(kThreads) void prefill_mfma_kernel(PrefillArgs a) {
+  __shared__ PrefillLds lds;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int col = lane & 15, kg = lane >> 4;
+  const int h = blockIdx.y, b = blockIdx.z;
+  const int G = a.G, ppw = kRows / G;  // positions per workgroup
+  const int64_t p0 = (int64_t)blockIdx.x * ppw;
+  const int64_t bh = (int64_t)b * a.H + h;
+  const int64_t T = a.T, L = a.n_q;
+  const int64_t qbase = T - L;  // position of query 0
+  const int sk = a.stride[0], sv = a.stride[1];
+  const float isk = a.inv_stride[0], isv = a.inv_stride[1];
+
+  const __amdgpu_buffer_rsrc_t r_kfk = make_rsrc(a.kf[0] + bh * a.cap_kf[0] * kD, (uint32_t)(a.cap_kf[0] * kD * 2));
+  const __amdgpu_buffer_rsrc_t r_kfv = make_rsrc(a.kf[1] + bh * a.cap_kf[1] * kD, (uint32_t)(a.cap_kf[1] * kD * 2));
+  const __amdgpu_buffer_rsrc_t r_pkk = make_rsrc(a.pk[0] + bh * a.cap_pf[0] * 16, (uint32_t)(a.cap_pf[0] * 64));
+  const __amdgpu_buffer_rsrc_t r_pkv = make_rsrc(a.pk[1] + bh * a.cap_pf[1] * 16, (uint32_t)(a.cap_pf[1] * 64));
+  const __amdgpu_buffer_rsrc_t r_sck = make_rsrc(a.sc[0] + bh * a.cap_pf[0], (uint32_t)(a.cap_pf[0] * 2));
+  const __amdgpu_buffer_rsrc_t r_scv = make_rsrc(a.sc[1] + bh * a.cap_pf[1], (uint32_t)(a.cap_pf[1] * 2));
+  uint32_t magic;  // fp16 1024 in both halves, an opaque VGPR for the byte permutes
+  asm volatile("v_mov_b32 %0, 0x64006400" : "=v"(magic));
+
+  // ---- Q fragment: row (16 wave + col), dims of K-step s in the grouped
+  // order; B operand of S^T = K . Q^T ----------------------------------------
+  const int my_row = 16 * wave + col;
+  const int64_t my_pos = p0 + my_row / G;
+  const int my_head = my_row % G;
+  const bool my_valid = my_pos < L;
+  h8_t qf[4];
+  {
+    const _Float16 sc16 = (_Float16)a.scale;
+    const uint16_t *qrow = a.q + (((int64_t)b * a.nq + h * G + my_head) * L + (my_valid ? my_pos : 0)) * kD;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      const uint4 u = *(const uint4 *)(qrow + 32 * s + 8 * kg);  // dims 32s + 8kg .. +7
+      const h8_t v = my_valid ? __builtin_bit_cast(h8_t, u) * sc16 : h8_t{};  // fp16(q * fp16(scale))
+      const uint4 w = __builtin_bit_cast(uint4, v);
+      qf[s] = h8_of(__builtin_amdgcn_perm(w.y, w.x, 0x05040100u), __builtin_amdgcn_perm(w.w, w.z, 0x05040100u),
+                    __builtin_amdgcn_perm(w.y, w.x, 0x07060302u), __builtin_amdgcn_perm(w.w, w.z, 0x07060302u));
+    }
+  }
+  // causal limit of this lane's row (scores rows = lane col)
+  const int64_t lim = a.causal ? qbase + my_pos : T - 1;
+
+  float m_run = -INFINITY, l_run = 0.f;
+  f4_t acc[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) acc[i] = f4_t{0.f, 0.f, 0.f, 0.f};
+
+  const int64_t last_pos = min(p0 + ppw, L) - 1;
+  const int64_t key_end = a.causal ? qbase + last_pos + 1 : T;  // keys [0, key_end)
+  const int64_t n_blocks = (key_end + kKeys - 1) / kKeys;
+
+  for (int64_t kb = 0; kb < n_blocks; ++kb) {
+    const int64_t k0 = kb * kKeys;
+    // ---- 1. rebuild the K and V blocks in LDS -----------------------------------
+    {
+      // K: thread -> key tid / 4, dims 32 (tid % 4) .. +31 (4 code words)
+      const int key = tid >> 2, qd = tid & 3;
+      const int t = (int)(k0 + key);
+      const bool in = t < T;
+      const int g = div_stride(t, sk, isk);
+      const int slot = (in && t != g * sk) ? t - g - 1 : -1;  // -1: I-frame / past the end
+      const uint32_t arow = in ? (uint32_t)g * 256u : 0x80000000u;
+      const h2_t s2 = as_h2(bload16(r_sck, (uint32_t)slot * 2u) * 0x10001u);
+      const uint4 cw = bload128(r_pkk, (uint32_t)slot * 64u + 16u * qd);
+      uint4 an[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) an[j] = bload128(r_kfk, arow + 64u * qd + 16u * j);
+      uint4 *dst = (uint4 *)&lds.k[key][32 * qd];
+      dst[0] = rebuild8(cw.x, an[0], s2, magic);
+      dst[1] = rebuild8(cw.y, an[1], s2, magic);
+      dst[2] = rebuild8(cw.z, an[2], s2, magic);
+      dst[3] = rebuild8(cw.w, an[3], s2, magic);
+    }
+    {
+      // V: thread -> code word w = tid % 16 (dims 8w .. 8w+7), keys 4 (tid / 16) .. +3
+      const int w = tid & 15, kq = tid >> 4;
+      uint4 r[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int t = (int)(k0 + 4 * kq + j);
+        const bool in = t < T;
+        const int g = div_stride(t, sv, isv);
+        const int slot = (in && t != g * sv) ? t - g - 1 : -1;
+        const uint32_t arow = in ? (uint32_t)g * 256u : 0x80000000u;
+        const h2_t s2 = as_h2(bload16(r_scv, (uint32_t)slot * 2u) * 0x10001u);
+        const uint32_t cw = bload32(r_pkv, (uint32_t)slot * 64u + 4u * w);
+        const uint4 an = bload128(r_kfv, arow + 16u * w);
+        r[j] = rebuild8(cw, an, s2, magic);
+      }
+      // transpose: row 8w + i of V^T holds grouped-order dim i of the 4 keys
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const int dw = i >> 1;
+        const uint32_t sel = (i & 1) ? 0x07060302u : 0x05040100u;
+        const uint32_t w0 = dw == 0 ? r[0].x : dw == 1 ? r[0].y : dw == 2 ? r[0].z : r[0].w;
+        const uint32_t w1 = dw == 0 ? r[1].x : dw == 1 ? r[1].y : dw == 2 ? r[1].z : r[1].w;
+        const uint32_t w2 = dw == 0 ? r[2].x : dw == 1 ? r[2].y : dw == 2 ? r[2].z : r[2].w;
+        const uint32_t w3 = dw == 0 ? r[3].x : dw == 1 ? r[3].y : dw == 2 ? r[3].z : r[3].w;
+        *(uint2 *)&lds.v[8 * w + i][4 * kq] =
+            uint2{__builtin_amdgcn_perm(w1, w0, sel), __builtin_amdgcn_perm(w3, w2, sel)};
+      }
+    }
+    __syncthreads();
+
+    // ---- 2. S^T = K . Q^T: lane (col = row, kg) gets keys 16t + 4kg + r ---------
+    float sc[4][4];
+    float mx = -INFINITY;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      f4_t d = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        const uint4 kv = *(const uint4 *)&lds.k[16 * t + col][32 * s + 8 * kg];
+        d = mfma32(__builtin_bit_cast(h8_t, kv), qf[s], d);
+      }
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int64_t key = k0 + 16 * t + 4 * kg + r;
+        // scores rounded to fp16 like the fallback's fp16 matmul, then log2
+        const float sv16 = (float)(_Float16)d[r];
+        sc[t][r] = key <= lim ? sv16 * kLog2e : -INFINITY;
+        mx = fmaxf(mx, sc[t][r]);
+      }
+    }
+    // ---- 3. online softmax (row max over the 4 lane groups of the column) -------
+    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    if (__any(mx > m_run + kTau)) {
+      const float m_new = fmaxf(m_run, mx);
+      const float f = (m_run == -INFINITY) ? 0.f : fast_exp2(m_run - m_new);
+      l_run *= f;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float fr = __shfl(f, 4 * kg + r, 64);  // factor of row 4kg + r
+#pragma unroll
+        for (int i = 0; i < 8; ++i) acc[i][r] *= fr;
+      }
+      m_run = m_new;
+    }
+    const float mref = (m_run == -INFINITY) ? 0.f : m_run;
+    h2_t pp[4][2];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      pp[t][0] = h2_t{(_Float16)fast_exp2(sc[t][0] - mref), (_Float16)fast_exp2(sc[t][1] - mref)};
+      pp[t][1] = h2_t{(_Float16)fast_exp2(sc[t][2] - mref), (_Float16)fast_exp2(sc[t][3] - mref)};
+      l_run += (float)pp[t][0].x + (float)pp[t][0].y + (float)pp[t][1].x + (float)pp[t][1].y;
+    }
+    // ---- 4. O += P . V: K index 8kg + e = key 16(2P) + 4kg + e (e < 4) or
+    // 16(2P+1) + 4kg + e - 4 --------------------------------------------------------
+#pragma unroll
+    for (int P = 0; P < 2; ++P) {
+      const h8_t ap = h8_of(as_u(pp[2 * P][0]), as_u(pp[2 * P][1]), as_u(pp[2 * P + 1][0]),
+                            as_u(pp[2 * P + 1][1]));
+#pragma unroll
+      for (int dt = 0; dt < 8; ++dt) {
+        const uint2 v0 = *(const uint2 *)&lds.v[16 * dt + col][16 * (2 * P) + 4 * kg];
+        const uint2 v1 = *(const uint2 *)&lds.v[16 * dt + col][16 * (2 * P + 1) + 4 * kg];
+        acc[dt] = mfma32(ap, h8_of(v0.x, v0.y, v1.x, v1.y), acc[dt]);
+      }
+    }
+    __syncthreads();  // the next block overwrites LDS
+  }
+
+  // ---- output: lane (col = grouped dim 16dt + col, kg) holds rows 4kg + r -------
+  l_run += __shfl_xor(l_run, 16, 64);
+  l_run += __shfl_xor(l_run, 32, 64);
+  const int perm8[8] = {0, 2, 4, 6, 1, 3, 5, 7};
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int row = 16 * wave + 4 * kg + r;
+    const int64_t pos = p0 + row / G;
+    const int head = row % G;
+    const float lr = __shfl(l_run, 4 * kg + r, 64);
+    const float inv = lr > 0.f ? 1.f / lr : 0.f;
+    if (pos < L) {
+      uint16_t *orow = a.out + (((int64_t)b * a.nq + h * G + head) * L + pos) * kD;
+#pragma unroll
+      for (int dt = 0; dt < 8; ++dt) {
+        const int gi = 16 * dt + col;
+        const int dim = 8 * (gi >> 3) + perm8[gi & 7];
+        orow[dim] = __builtin_bit_cast(uint16_t, (_Float16)(acc[dt][r] * inv));
+      }
+    }
+  }
+}
+
+}  // namespace
+}  // namespace cq
+
+using namespace cq;
+
+extern "C" int cq_prefill_attn(const cq_cache_desc *cache, const void *q, int32_t q_dtype,
+                               int32_t n_q_heads, int64_t n_q, float scale, int32_t causal,
+                               int64_t seq_len, void *out, cq_stream_t stream) {
+  int st = validate_cache(cache);
+  if (st) return st;
+  if (!q || !out) return CQ_ERR_ARG;
+  if (q_dtype != CQ_F16) return CQ_ERR_DTYPE;
+  if (cache->head_dim != kD) return CQ_ERR_UNSUPPORTED;
+  if (n_q_heads < 1 || n_q_heads % cache->n_kv_heads) return CQ_ERR_SHAPE;
+  const int G = n_q_heads / cache->n_kv_heads;
+  if (G > kRows || kRows % G) return CQ_ERR_UNSUPPORTED;
+  if (n_q < 1 || seq_len < n_q || seq_len >= (1 << 24)) return CQ_ERR_SHAPE;
+  if (((uintptr_t)q | (uintptr_t)out) & 15) return CQ_ERR_ALIGN;
+  PrefillArgs a;
+  const cq_component *cp[2] = {&cache->k, &cache->v};
+  for (int i = 0; i < 2; ++i) {
+    a.kf[i] = cp[i]->keyframes;
+    a.pk[i] = cp[i]->packed;
+    a.sc[i] = cp[i]->scales;
+    a.cap_kf[i] = cp[i]->cap_keyframes;
+    a.cap_pf[i] = cp[i]->cap_pframes;
+    a.stride[i] = cp[i]->stride;
+    a.inv_stride[i] = 1.0f / (float)cp[i]->stride;
+    if (num_keyframes(seq_len, a.stride[i]) > a.cap_kf[i] ||
+        num_pframes(seq_len, a.stride[i]) > a.cap_pf[i])
+      return CQ_ERR_CAPACITY;
+    // buffer resources address each (sequence, head) region with 32-bit offsets
+    if (a.cap_kf[i] * kD * 2 >= ((int64_t)1 << 31) || a.cap_pf[i] * 64 >= ((int64_t)1 << 31))
+      return CQ_ERR_UNSUPPORTED;
+  }
+  a.B = cache->batch;
+  a.H = cache->n_kv_heads;
+  a.G = G;
+  a.nq = n_q_heads;
+  a.n_q = n_q;
+  a.T = seq_len;
+  a.causal = causal ? 1 : 0;
+  a.scale = scale;
+  a.q = (const uint16_t *)q;
+  a.out = (uint16_t *)out;
+  const int ppw = kRows / G;
+  const dim3 grid((unsigned)((n_q + ppw - 1) / ppw), (unsigned)a.H, (unsigned)a.B);
+  prefill_mfma_kernel<<<grid, dim3(kThreads), 0, (hipStream_t)stream>>>(a);
+  return hipGetLastError() == hipSuccess ? CQ_OK : CQ_ERR_LAUNCH;
+}

@@ -85,3 +85,30 @@ def chronoquant_sdpa_kernel(q: torch.Tensor, cache, scale: float = 1.0,
               cache.offset, max_len, out.data_ptr(), _lib.dtype_code(out.dtype),
               ws.data_ptr(), ws.numel(), _lib.stream_of(q))
     return out
+
+
+def chronoquant_prefill_kernel(q: torch.Tensor, cache, scale: float = 1.0,
+                               causal: bool = True) -> torch.Tensor:
+    """Chunked-prefill attention over a ChronoQuantCache (cq_prefill_attn).
+
+    q: [B, nq, L, 128] fp16 UNSCALED; the L queries are the cache's last L
+    tokens (already appended).  Causal (query i sees keys <= offset - L + i)
+    or full attention.  Same result semantics as the reconstruct fallback of
+    chronoquant_sdpa (attention.py:61-74).  Returns [B, nq, L, 128] fp16.
+    """
+    _lib.require_gpu(q)
+    q = q.contiguous()
+    B, nq, L, D = q.shape
+    out = torch.empty_like(q)
+    _lib.call("cq_prefill_attn", cache._descriptor(), q.data_ptr(), _lib.dtype_code(q.dtype), nq,
+              L, float(scale), int(bool(causal)), cache.offset, out.data_ptr(), _lib.stream_of(q))
+    return out
+
+
+def prefill_supported(queries: torch.Tensor, cache, mask) -> bool:
+    """Whether cq_prefill_attn serves this chronoquant_sdpa call."""
+    B, nq, L, D = queries.shape
+    return (L > 1 and D == 128 and queries.dtype == torch.float16
+            and (mask is None or (isinstance(mask, str) and mask == "causal"))
+            and cache.offset >= L and nq % cache._shape[1] == 0
+            and 64 % (nq // cache._shape[1]) == 0)

@@ -163,6 +163,20 @@ int cq_fp16_decode_attn(const uint16_t *k, const uint16_t *v,
                         int32_t out_dtype, void *workspace,
                         size_t workspace_bytes, cq_stream_t stream);
 
+/* Chunked-prefill attention over the compressed cache: the n_q query tokens
+ * of every sequence are its last n_q cached tokens (positions seq_len - n_q
+ * .. seq_len - 1, appended before the call), attending causally (query i
+ * sees keys <= seq_len - n_q + i) or, with causal = 0, to all seq_len keys.
+ * Replaces the reconstruct fallback of chronoquant_sdpa for q_len > 1 with
+ * mask None or "causal" (reference attention.py:61-74 over cache.py:131-160):
+ * K/V rebuilt as fp16(anchor + fp16(fp16(code) * scale)), q' = fp16(q *
+ * fp16(scale)), fp16 scores, fp32 softmax, fp16 weights, fp16 output.
+ * head_dim 128, fp16 q, n_q_heads / n_kv_heads dividing 64.
+ * q, out: fp16 [B][n_q_heads][n_q][128], 16-byte aligned. */
+int cq_prefill_attn(const cq_cache_desc *cache, const void *q, int32_t q_dtype,
+                    int32_t n_q_heads, int64_t n_q, float scale, int32_t causal,
+                    int64_t seq_len, void *out, cq_stream_t stream);
+
 /* Static description of a status code. */
 const char *cq_status_string(int32_t status);
 

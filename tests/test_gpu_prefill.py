@@ -1,0 +1,105 @@
+"""GPU parity of the chunked-prefill kernel (cq_prefill_attn) against the
+oracle's restatement of the reference's reconstruct fallback for q_len > 1
+(attention.py:61-74 with the causal mask of attention.py:12-16, over
+cache.py:131-160), and against the torch fallback path of chronoquant_sdpa.
+
+Bar: |got - ref| <= 2e-3 + 1e-2 |ref| elementwise and relative L2 <= 1e-2
+(the north-star attention tolerance).  The kernel rounds scores to fp16 as
+the fallback does; its softmax is the online form with fp16 weights.
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as O
+from tests.cqtest import assert_close, build_gpu_cache, build_oracle, to_gpu
+
+pytestmark = pytest.mark.gpu
+
+
+def _data(seed, B, H, T, D):
+    rng = np.random.default_rng(seed)
+    k = np.cumsum(rng.standard_normal((B, H, T, D)) * 0.1, axis=2).astype(np.float16)
+    v = np.cumsum(rng.standard_normal((B, H, T, D)) * 0.1, axis=2).astype(np.float16)
+    return k, v
+
+
+def _check(B, H, G, T, L, params, causal=True, seed=0, chunks=None):
+    from chronoquant_mlx_amd.kernels import chronoquant_prefill_kernel
+    D = 128
+    k, v = _data(seed, B, H, T, D)
+    q = np.random.default_rng(seed + 1).standard_normal((B, G * H, L, D)).astype(np.float16)
+    cache = build_gpu_cache(k, v, chunks=chunks, **params)
+    scale = D ** -0.5
+    out = chronoquant_prefill_kernel(to_gpu(q), cache, scale, causal=causal).float().cpu().numpy()
+    for b in range(B):
+        ck, cv = build_oracle(k[b], v[b], **params)
+        ref = O.sdpa_fallback(q[b], ck.reconstruct(), cv.reconstruct(), scale, causal=causal)
+        assert_close(out[b], ref.astype(np.float64), what=f"b={b} T={T} L={L} {params}")
+    return out
+
+
+@pytest.mark.parametrize("G,H", [(1, 8), (4, 8), (8, 2), (16, 1)])
+def test_gqa_ratios(G, H):
+    _check(1, H, G, 700, 128, dict(stride_k=32, stride_v=8), seed=G)
+
+
+@pytest.mark.parametrize("params", [dict(stride_k=64, stride_v=32, bits_v=3, dz_v=0.05),
+                                    dict(stride_k=1, stride_v=8),
+                                    dict(stride_k=5, stride_v=12),
+                                    dict(stride_k=4, stride_v=4, bits_k=3, bits_v=3, dz_k=0.2,
+                                         dz_v=0.2)])
+def test_codec_settings(params):
+    _check(1, 2, 4, 600, 100, params, seed=7)
+
+
+@pytest.mark.parametrize("T,L", [(2, 2), (65, 64), (64, 64), (513, 512), (1000, 37), (300, 300)])
+def test_lengths(T, L):
+    # chunks that do not fill a position block, whole prompts, block edges
+    _check(1, 2, 4, T, L, dict(stride_k=32, stride_v=8), seed=T + L)
+
+
+def test_batch_and_full_attention():
+    _check(2, 2, 4, 500, 96, dict(stride_k=32, stride_v=8), causal=False, seed=3)
+    _check(2, 2, 4, 500, 96, dict(stride_k=32, stride_v=8), causal=True, seed=4)
+
+
+def test_chunked_prefill_sequence():
+    # the prompt arrives in 3 chunks; after each append the chunk's queries
+    # attend causally to everything cached so far
+    from chronoquant_mlx_amd import ChronoQuantCache
+    from chronoquant_mlx_amd.kernels import chronoquant_prefill_kernel
+    H, G, D, T = 2, 4, 128, 640
+    params = dict(stride_k=32, stride_v=8)
+    k, v = _data(9, 1, H, T, D)
+    q = np.random.default_rng(10).standard_normal((1, G * H, T, D)).astype(np.float16)
+    cache = ChronoQuantCache(stride_k=32, stride_v=8, dead_zone_v=0.0)
+    ck, cv = build_oracle(k[0], v[0], **params)
+    rk, rv = ck.reconstruct(), cv.reconstruct()
+    pos = 0
+    for L in (200, 256, 184):
+        cache.update_and_fetch(to_gpu(k[:, :, pos:pos + L]), to_gpu(v[:, :, pos:pos + L]))
+        out = chronoquant_prefill_kernel(to_gpu(q[:, :, pos:pos + L]), cache, D ** -0.5)
+        ref = O.sdpa_fallback(q[0, :, pos:pos + L], rk[:, :pos + L], rv[:, :pos + L], D ** -0.5,
+                              causal=True)
+        assert_close(out.float().cpu().numpy()[0], ref.astype(np.float64), what=f"chunk at {pos}")
+        pos += L
+
+
+@pytest.mark.parametrize("mask", ["causal", None])
+def test_sdpa_routes_prefill_and_matches_fallback(mask):
+    from chronoquant_mlx_amd import attention as A
+    H, G, T, L, D = 2, 4, 400, 64, 128
+    params = dict(stride_k=32, stride_v=8)
+    k, v = _data(11, 1, H, T, D)
+    cache = build_gpu_cache(k, v, **params)
+    q = to_gpu(np.random.default_rng(12).standard_normal((1, G * H, L, D)).astype(np.float16))
+    A.PREFILL_KERNEL = True
+    try:
+        got = A.chronoquant_sdpa(q, None, None, cache, D ** -0.5, mask=mask)
+        A.PREFILL_KERNEL = False
+        ref = A.chronoquant_sdpa(q, None, None, cache, D ** -0.5, mask=mask)
+    finally:
+        A.PREFILL_KERNEL = True
+    assert_close(got.float().cpu().numpy(), ref.float().cpu().numpy().astype(np.float64),
+                 what=f"mask={mask}")
