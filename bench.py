@@ -285,6 +285,51 @@ def time_streaming(name, dev, stream, n_steps=256):
     return res
 
 
+def time_prefill(dev, stream, steps, T=8192, L=512):
+    """Chunked-prefill attention (cq_prefill_attn) on configs[4]'s shape: the
+    last L-token chunk of a T-token prompt, GQA 32q/8kv, Full-Throttle V3
+    codec; against the reconstruct fallback (cq_reconstruct + dense torch
+    attention) on the same call."""
+    import dataclasses
+
+    import torch
+
+    from chronoquant_mlx_amd import attention as A
+    from chronoquant_mlx_amd import synth
+    from chronoquant_mlx_amd.kernels import chronoquant_prefill_kernel
+    cfg = dataclasses.replace(synth.CONFIGS["ftv3_16k"], T=T)
+    cache, kt, vt = build_cache_device(cfg, dev)
+    del kt, vt
+    nq, D, H = cfg.n_q_heads, cfg.head_dim, cfg.n_kv_heads
+    q = torch.randn(1, nq, L, D, device=dev).half()
+    scale = D ** -0.5
+    # causal FLOPs: QK^T and PV, 2 flops per MAC, query i sees T - L + i + 1 keys
+    keys = L * (T - L) + L * (L + 1) // 2
+    flops = 4 * D * nq * keys
+    ms = time_graph([lambda: chronoquant_prefill_kernel(q, cache, scale, causal=True)],
+                    steps, 3, stream)
+    A.PREFILL_KERNEL = False
+    try:
+        # eager: the fallback creates small host-side tensors (not capturable)
+        ms_fb = time_eager([lambda: A.chronoquant_sdpa(q, None, None, cache, scale, mask="causal")],
+                           max(5, steps // 10), 2, stream)
+    finally:
+        A.PREFILL_KERNEL = True
+    tf = flops / (ms * 1e-3) / 1e12
+    log(f"[bench] prefill T={T} L={L}: {ms * 1e3:.1f} us ({tf:.1f} TFLOP/s), "
+        f"reconstruct fallback {ms_fb * 1e3:.1f} us")
+    res = {"workload": f"B=1 GQA {nq}q/{H}kv D={D}: last {L}-token chunk of a {T}-token prompt, "
+                       f"causal, strides {cfg.stride_k}/{cfg.stride_v} bits "
+                       f"{cfg.delta_bits_k}/{cfg.delta_bits_v}",
+           "us_per_call": round(ms * 1e3, 2), "TFLOPs": round(tf, 2),
+           "frac_of_fp16_mfma_peak": round(tf / 2500.0, 4), "flops_per_call": flops,
+           "reconstruct_fallback_us": round(ms_fb * 1e3, 2),
+           "speedup_vs_fallback": round(ms_fb / ms, 2)}
+    del cache
+    torch.cuda.empty_cache()
+    return res
+
+
 def cpu_baseline(cfg, k, v, q, budget_s=12.0):
     from oracle import oracle as O
     threads = min(16, len(os.sched_getaffinity(0)))
@@ -428,6 +473,7 @@ def main():
         extra["c2"] = time_decode_config("c2", dev, stream, args.steps, args.warmup, timer,
                                          device_gen=True)
         extra["c3"] = time_streaming("c3", dev, stream)
+        extra["prefill"] = time_prefill(dev, stream, 50)
         result["extra"] = extra
 
     if not args.no_cpu_baseline:

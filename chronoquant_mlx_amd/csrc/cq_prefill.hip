@@ -159,44 +159,58 @@ __global__ __launch_bounds__(kThreads) void prefill_mfma_kernel(PrefillArgs a) {
   const int64_t key_end = a.causal ? qbase + last_pos + 1 : T;  // keys [0, key_end)
   const int64_t n_blocks = (key_end + kKeys - 1) / kKeys;
 
-  for (int64_t kb = 0; kb < n_blocks; ++kb) {
-    const int64_t k0 = kb * kKeys;
-    // ---- 1. rebuild the K and V blocks in LDS -----------------------------------
+  // Raw block data in registers: the next block's loads are issued right
+  // after the current block has been rebuilt into LDS, so they arrive while
+  // the current block's products run.
+  //   K: thread -> key tid / 4, dims 32 (tid % 4) .. +31 (4 code words)
+  //   V: thread -> code word tid % 16 (dims 8w .. 8w+7), keys 4 (tid / 16) .. +3
+  const int kkey = tid >> 2, kqd = tid & 3;
+  const int vw = tid & 15, vkq = tid >> 4;
+  uint4 k_cw, k_an[4];
+  uint32_t k_s;
+  uint32_t v_cw[4], v_s[4];
+  uint4 v_an[4];
+  auto load_block = [&](int64_t k0) {
     {
-      // K: thread -> key tid / 4, dims 32 (tid % 4) .. +31 (4 code words)
-      const int key = tid >> 2, qd = tid & 3;
-      const int t = (int)(k0 + key);
+      const int t = (int)(k0 + kkey);
       const bool in = t < T;
       const int g = div_stride(t, sk, isk);
       const int slot = (in && t != g * sk) ? t - g - 1 : -1;  // -1: I-frame / past the end
       const uint32_t arow = in ? (uint32_t)g * 256u : 0x80000000u;
-      const h2_t s2 = as_h2(bload16(r_sck, (uint32_t)slot * 2u) * 0x10001u);
-      const uint4 cw = bload128(r_pkk, (uint32_t)slot * 64u + 16u * qd);
-      uint4 an[4];
+      k_s = bload16(r_sck, (uint32_t)slot * 2u);
+      k_cw = bload128(r_pkk, (uint32_t)slot * 64u + 16u * kqd);
 #pragma unroll
-      for (int j = 0; j < 4; ++j) an[j] = bload128(r_kfk, arow + 64u * qd + 16u * j);
-      uint4 *dst = (uint4 *)&lds.k[key][32 * qd];
-      dst[0] = rebuild8(cw.x, an[0], s2, magic);
-      dst[1] = rebuild8(cw.y, an[1], s2, magic);
-      dst[2] = rebuild8(cw.z, an[2], s2, magic);
-      dst[3] = rebuild8(cw.w, an[3], s2, magic);
+      for (int j = 0; j < 4; ++j) k_an[j] = bload128(r_kfk, arow + 64u * kqd + 16u * j);
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int t = (int)(k0 + 4 * vkq + j);
+      const bool in = t < T;
+      const int g = div_stride(t, sv, isv);
+      const int slot = (in && t != g * sv) ? t - g - 1 : -1;
+      const uint32_t arow = in ? (uint32_t)g * 256u : 0x80000000u;
+      v_s[j] = bload16(r_scv, (uint32_t)slot * 2u);
+      v_cw[j] = bload32(r_pkv, (uint32_t)slot * 64u + 4u * vw);
+      v_an[j] = bload128(r_kfv, arow + 16u * vw);
+    }
+  };
+  if (n_blocks > 0) load_block(0);
+
+  for (int64_t kb = 0; kb < n_blocks; ++kb) {
+    const int64_t k0 = kb * kKeys;
+    // ---- 1. rebuild the K and V blocks in LDS -----------------------------------
+    {
+      const h2_t s2 = as_h2(k_s * 0x10001u);
+      uint4 *dst = (uint4 *)&lds.k[kkey][32 * kqd];
+      dst[0] = rebuild8(k_cw.x, k_an[0], s2, magic);
+      dst[1] = rebuild8(k_cw.y, k_an[1], s2, magic);
+      dst[2] = rebuild8(k_cw.z, k_an[2], s2, magic);
+      dst[3] = rebuild8(k_cw.w, k_an[3], s2, magic);
     }
     {
-      // V: thread -> code word w = tid % 16 (dims 8w .. 8w+7), keys 4 (tid / 16) .. +3
-      const int w = tid & 15, kq = tid >> 4;
       uint4 r[4];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int t = (int)(k0 + 4 * kq + j);
-        const bool in = t < T;
-        const int g = div_stride(t, sv, isv);
-        const int slot = (in && t != g * sv) ? t - g - 1 : -1;
-        const uint32_t arow = in ? (uint32_t)g * 256u : 0x80000000u;
-        const h2_t s2 = as_h2(bload16(r_scv, (uint32_t)slot * 2u) * 0x10001u);
-        const uint32_t cw = bload32(r_pkv, (uint32_t)slot * 64u + 4u * w);
-        const uint4 an = bload128(r_kfv, arow + 16u * w);
-        r[j] = rebuild8(cw, an, s2, magic);
-      }
+      for (int j = 0; j < 4; ++j) r[j] = rebuild8(v_cw[j], v_an[j], as_h2(v_s[j] * 0x10001u), magic);
       // transpose: row 8w + i of V^T holds grouped-order dim i of the 4 keys
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
@@ -206,10 +220,11 @@ __global__ __launch_bounds__(kThreads) void prefill_mfma_kernel(PrefillArgs a) {
         const uint32_t w1 = dw == 0 ? r[1].x : dw == 1 ? r[1].y : dw == 2 ? r[1].z : r[1].w;
         const uint32_t w2 = dw == 0 ? r[2].x : dw == 1 ? r[2].y : dw == 2 ? r[2].z : r[2].w;
         const uint32_t w3 = dw == 0 ? r[3].x : dw == 1 ? r[3].y : dw == 2 ? r[3].z : r[3].w;
-        *(uint2 *)&lds.v[8 * w + i][4 * kq] =
+        *(uint2 *)&lds.v[8 * vw + i][4 * vkq] =
             uint2{__builtin_amdgcn_perm(w1, w0, sel), __builtin_amdgcn_perm(w3, w2, sel)};
       }
     }
+    if (kb + 1 < n_blocks) load_block(k0 + kKeys);
     __syncthreads();
 
     // ---- 2. S^T = K . Q^T: lane (col = row, kg) gets keys 16t + 4kg + r ---------
