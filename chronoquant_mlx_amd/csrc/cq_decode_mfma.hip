@@ -67,6 +67,27 @@ __device__ __forceinline__ h8_t h8_of(uint32_t a, uint32_t b, uint32_t c, uint32
   return h8_t{x.x, x.y, y.x, y.y, z.x, z.y, w.x, w.y};
 }
 
+// bf16 queries: q' = bf16(q * bf16(scale)) (attention.py:46 in bf16: the
+// fp32 product of two bf16 values is exact, so one round-to-nearest-even to
+// bf16 gives the bf16 product), then converted to fp16 for the MFMA operand.
+// The conversion is exact for |q'| in fp16's normal range (bf16 carries 8
+// significant bits, fp16 11); below 2^-14 fp16 subnormals keep fewer bits.
+__device__ __forceinline__ float bf16_round(float f) {
+  uint32_t u = __float_as_uint(f);
+  u += 0x7FFFu + ((u >> 16) & 1u);
+  return __uint_as_float(u & 0xFFFF0000u);
+}
+__device__ __forceinline__ h8_t bf16x8_scaled_to_f16(uint4 raw, float scb) {
+  const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
+  h8_t r;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    r[2 * i] = (_Float16)bf16_round(__uint_as_float(w[i] << 16) * scb);
+    r[2 * i + 1] = (_Float16)bf16_round(__uint_as_float(w[i] & 0xFFFF0000u) * scb);
+  }
+  return r;
+}
+
 // (x & m) | o.  With o an opaque VGPR value (the magic below) the compiler
 // emits one v_and_or_b32 (mask in an SGPR: gfx9 VOP3 reads at most one
 // SGPR/literal).  The instruction itself must stay compiler-generated: the
@@ -355,10 +376,14 @@ __global__ __launch_bounds__(kThreadsMfma) void decode_mfma_kernel(DecodeArgs a)
   float s8 = 0.f;
   auto prep_q = [&]() {
     const _Float16 sc16 = qok ? (_Float16)a.scale : (_Float16)0.f;
+    const float scb = qok ? bf16_round(a.scale) : 0.f;
+    const bool bf = a.q_dtype == CQ_BF16;
     float qs = 0.f;
 #pragma unroll
     for (int kb = 0; kb < 4; ++kb) {
-      const h8_t v = __builtin_bit_cast(h8_t, qraw[kb]) * sc16;  // fp16(q * fp16(scale))
+      // fp16 q: fp16(q * fp16(scale)); bf16 q: bf16(q * bf16(scale)) as fp16
+      const h8_t v = bf ? bf16x8_scaled_to_f16(qraw[kb], scb)
+                        : __builtin_bit_cast(h8_t, qraw[kb]) * sc16;
       qc[kb] = h8_t{v[0], v[4], v[1], v[5], v[2], v[6], v[3], v[7]};
 #pragma unroll
       for (int e = 0; e < 8; ++e) qs += (float)v[e];
@@ -678,7 +703,9 @@ __global__ __launch_bounds__(kThreadsMfma) void decode_plain_kernel(DecodeArgs a
 static bool plain_mode(const DecodeArgs &a) { return a.stride[0] == 1 && a.stride[1] == 1; }
 
 bool mfma_supported(const DecodeArgs &a) {
-  if (a.D != kD || a.q_dtype != CQ_F16) return false;
+  if (a.D != kD) return false;
+  // compressed cache: fp16 or bf16 queries; fp16 baseline: fp16 queries
+  if (a.q_dtype != CQ_F16 && !(a.q_dtype == CQ_BF16 && !plain_mode(a))) return false;
   if (a.max_T >= (1 << 24)) return false;
   // buffer resources address each (sequence, head) region with 32-bit offsets
   for (int i = 0; i < 2; ++i)

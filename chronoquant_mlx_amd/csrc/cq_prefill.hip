@@ -1,5 +1,5 @@
 // cq_prefill.hip — gfx950 chunked-prefill attention over the ChronoQuant cache
-// (head_dim 128, fp16 queries): the last n_q cached tokens of every sequence
+// (head_dim 128, fp16 or bf16 queries): the last n_q cached tokens of every sequence
 // attend to the cache, causally or to all of it.
 //
 // Reference semantics: the reconstruct fallback of chronoquant_sdpa for
@@ -55,9 +55,22 @@ struct PrefillArgs {
   int64_t n_q, T;
   int causal;
   float scale;
-  const uint16_t *q;  // [B][nq][n_q][D] fp16
-  uint16_t *out;      // [B][nq][n_q][D] fp16
+  const uint16_t *q;  // [B][nq][n_q][D] fp16 or bf16
+  uint16_t *out;      // [B][nq][n_q][D], the dtype of q
 };
+
+// bf16 q' = bf16(q * bf16(scale)) (one rounding of the exact fp32 product),
+// then fp16 for the MFMA operand (exact for |q'| in fp16's normal range).
+__device__ __forceinline__ float bf16_round(float f) {
+  uint32_t u = __float_as_uint(f);
+  u += 0x7FFFu + ((u >> 16) & 1u);
+  return __uint_as_float(u & 0xFFFF0000u);
+}
+__device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
+  uint32_t u = __float_as_uint(f);
+  u += 0x7FFFu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
 
 __device__ __forceinline__ h2_t as_h2(uint32_t u) { return __builtin_bit_cast(h2_t, u); }
 __device__ __forceinline__ uint32_t as_u(h2_t h) { return __builtin_bit_cast(uint32_t, h); }
@@ -106,6 +119,9 @@ struct alignas(16) PrefillLds {
   uint16_t v[kD][kVStride];     // V block transposed, [dim (grouped order)][key]
 };
 
+// Bf16: queries (and output) are bf16.  The reference then computes the
+// scores in fp32 (bf16 x fp16 promotes), so they are not rounded to fp16.
+template <bool Bf16>
 __global__ __launch_bounds__(kThreads) void prefill_mfma_kernel(PrefillArgs a) {
   __shared__ PrefillLds lds;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -137,11 +153,23 @@ __global__ __launch_bounds__(kThreads) void prefill_mfma_kernel(PrefillArgs a) {
   h8_t qf[4];
   {
     const _Float16 sc16 = (_Float16)a.scale;
+    const float scb = bf16_round(a.scale);
     const uint16_t *qrow = a.q + (((int64_t)b * a.nq + h * G + my_head) * L + (my_valid ? my_pos : 0)) * kD;
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
       const uint4 u = *(const uint4 *)(qrow + 32 * s + 8 * kg);  // dims 32s + 8kg .. +7
-      const h8_t v = my_valid ? __builtin_bit_cast(h8_t, u) * sc16 : h8_t{};  // fp16(q * fp16(scale))
+      h8_t v;
+      if (Bf16) {
+        const uint32_t w4[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          v[2 * i] = (_Float16)bf16_round(__uint_as_float(w4[i] << 16) * scb);
+          v[2 * i + 1] = (_Float16)bf16_round(__uint_as_float(w4[i] & 0xFFFF0000u) * scb);
+        }
+      } else {
+        v = __builtin_bit_cast(h8_t, u) * sc16;  // fp16(q * fp16(scale))
+      }
+      if (!my_valid) v = h8_t{};
       const uint4 w = __builtin_bit_cast(uint4, v);
       qf[s] = h8_of(__builtin_amdgcn_perm(w.y, w.x, 0x05040100u), __builtin_amdgcn_perm(w.w, w.z, 0x05040100u),
                     __builtin_amdgcn_perm(w.y, w.x, 0x07060302u), __builtin_amdgcn_perm(w.w, w.z, 0x07060302u));
@@ -241,8 +269,8 @@ __global__ __launch_bounds__(kThreads) void prefill_mfma_kernel(PrefillArgs a) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int64_t key = k0 + 16 * t + 4 * kg + r;
-        // scores rounded to fp16 like the fallback's fp16 matmul, then log2
-        const float sv16 = (float)(_Float16)d[r];
+        // fp16 q: scores rounded to fp16 like the fallback's fp16 matmul
+        const float sv16 = Bf16 ? d[r] : (float)(_Float16)d[r];
         sc[t][r] = key <= lim ? sv16 * kLog2e : -INFINITY;
         mx = fmaxf(mx, sc[t][r]);
       }
@@ -303,7 +331,8 @@ __global__ __launch_bounds__(kThreads) void prefill_mfma_kernel(PrefillArgs a) {
       for (int dt = 0; dt < 8; ++dt) {
         const int gi = 16 * dt + col;
         const int dim = 8 * (gi >> 3) + perm8[gi & 7];
-        orow[dim] = __builtin_bit_cast(uint16_t, (_Float16)(acc[dt][r] * inv));
+        orow[dim] = Bf16 ? f32_to_bf16_bits(acc[dt][r] * inv)
+                         : __builtin_bit_cast(uint16_t, (_Float16)(acc[dt][r] * inv));
       }
     }
   }
@@ -320,7 +349,7 @@ extern "C" int cq_prefill_attn(const cq_cache_desc *cache, const void *q, int32_
   int st = validate_cache(cache);
   if (st) return st;
   if (!q || !out) return CQ_ERR_ARG;
-  if (q_dtype != CQ_F16) return CQ_ERR_DTYPE;
+  if (q_dtype != CQ_F16 && q_dtype != CQ_BF16) return CQ_ERR_DTYPE;
   if (cache->head_dim != kD) return CQ_ERR_UNSUPPORTED;
   if (n_q_heads < 1 || n_q_heads % cache->n_kv_heads) return CQ_ERR_SHAPE;
   const int G = n_q_heads / cache->n_kv_heads;
@@ -356,6 +385,9 @@ extern "C" int cq_prefill_attn(const cq_cache_desc *cache, const void *q, int32_
   a.out = (uint16_t *)out;
   const int ppw = kRows / G;
   const dim3 grid((unsigned)((n_q + ppw - 1) / ppw), (unsigned)a.H, (unsigned)a.B);
-  prefill_mfma_kernel<<<grid, dim3(kThreads), 0, (hipStream_t)stream>>>(a);
+  if (q_dtype == CQ_BF16)
+    prefill_mfma_kernel<true><<<grid, dim3(kThreads), 0, (hipStream_t)stream>>>(a);
+  else
+    prefill_mfma_kernel<false><<<grid, dim3(kThreads), 0, (hipStream_t)stream>>>(a);
   return hipGetLastError() == hipSuccess ? CQ_OK : CQ_ERR_LAUNCH;
 }

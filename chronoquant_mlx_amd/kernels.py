@@ -91,10 +91,11 @@ def chronoquant_prefill_kernel(q: torch.Tensor, cache, scale: float = 1.0,
                                causal: bool = True) -> torch.Tensor:
     """Chunked-prefill attention over a ChronoQuantCache (cq_prefill_attn).
 
-    q: [B, nq, L, 128] fp16 UNSCALED; the L queries are the cache's last L
-    tokens (already appended).  Causal (query i sees keys <= offset - L + i)
-    or full attention.  Same result semantics as the reconstruct fallback of
-    chronoquant_sdpa (attention.py:61-74).  Returns [B, nq, L, 128] fp16.
+    q: [B, nq, L, 128] fp16 or bf16 UNSCALED; the L queries are the cache's
+    last L tokens (already appended).  Causal (query i sees keys <= offset -
+    L + i) or full attention.  Same result semantics as the reconstruct
+    fallback of chronoquant_sdpa (attention.py:61-74).  Returns
+    [B, nq, L, 128] of q's dtype.
     """
     _lib.require_gpu(q)
     q = q.contiguous()
@@ -108,7 +109,7 @@ def chronoquant_prefill_kernel(q: torch.Tensor, cache, scale: float = 1.0,
 def prefill_supported(queries: torch.Tensor, cache, mask) -> bool:
     """Whether cq_prefill_attn serves this chronoquant_sdpa call."""
     B, nq, L, D = queries.shape
-    return (L > 1 and D == 128 and queries.dtype == torch.float16
+    return (L > 1 and D == 128 and queries.dtype in (torch.float16, torch.bfloat16)
             and (mask is None or (isinstance(mask, str) and mask == "causal"))
             and cache.offset >= L and nq % cache._shape[1] == 0
             and 64 % (nq // cache._shape[1]) == 0)

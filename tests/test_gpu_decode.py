@@ -236,3 +236,31 @@ def test_patch_routes_chronoquant_caches():
     finally:
         cq.revert()
     assert host.scaled_dot_product_attention is not None
+
+
+def test_bf16_queries():
+    # bf16 queries: q' = bf16(q * bf16(scale)) (attention.py:46 in bf16), fed to
+    # the MFMA kernel as fp16 (exact in fp16's normal range) and to the
+    # portable kernel as fp32; both against binary64 attention on the fp16
+    # reconstruction with the same q'
+    from chronoquant_mlx_amd.kernels import chronoquant_sdpa_kernel
+    rng = np.random.default_rng(17)
+    B, H, T, D, G = 2, 2, 900, 128, 4
+    k = np.cumsum(rng.standard_normal((B, H, T, D)) * 0.1, axis=2).astype(np.float16)
+    v = np.cumsum(rng.standard_normal((B, H, T, D)) * 0.1, axis=2).astype(np.float16)
+    q32 = rng.standard_normal((B, G * H, D)).astype(np.float32)
+    params = dict(stride_k=32, stride_v=8)
+    cache = build_gpu_cache(k, v, **params)
+    scale = D ** -0.5
+    qb = torch.from_numpy(q32).to("cuda").to(torch.bfloat16)
+    out_m = chronoquant_sdpa_kernel(qb, cache, scale).float().cpu().numpy()
+    out_g = chronoquant_sdpa_kernel(qb, cache, scale, generic=True).float().cpu().numpy()
+    scb = torch.tensor(scale, dtype=torch.bfloat16)
+    qprime = (qb.cpu() * scb).to(torch.float16).numpy()  # bf16 product, exactly representable
+    for b in range(B):
+        ck, cv = build_oracle(k[b], v[b], **params)
+        exact = O.sdpa_exact(qprime[b], ck.reconstruct(), cv.reconstruct(), 1.0)
+        # bf16 output rounding: 2^-9 relative
+        assert_close(out_m[b], exact, 2e-3, 1e-2, what=f"mfma b={b}")
+        assert_close(out_g[b], exact, 2e-3, 1e-2, what=f"generic b={b}")
+        assert_close(out_m[b], out_g[b], 5e-4, 5e-3, what=f"mfma vs generic b={b}")

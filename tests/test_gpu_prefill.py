@@ -103,3 +103,23 @@ def test_sdpa_routes_prefill_and_matches_fallback(mask):
         A.PREFILL_KERNEL = True
     assert_close(got.float().cpu().numpy(), ref.float().cpu().numpy().astype(np.float64),
                  what=f"mask={mask}")
+
+
+@pytest.mark.parametrize("causal", [True, False])
+def test_bf16_queries(causal):
+    # bf16 queries: q' = bf16(q * bf16(scale)), fp32 scores (the reference's
+    # bf16 x fp16 promotion), bf16 output; against the oracle fallback on the
+    # same q' (exact in fp16) with scale 1
+    from chronoquant_mlx_amd.kernels import chronoquant_prefill_kernel
+    B, H, G, T, L, D = 1, 2, 4, 700, 130, 128
+    params = dict(stride_k=64, stride_v=32, bits_v=3, dz_v=0.05)
+    k, v = _data(21, B, H, T, D)
+    q32 = np.random.default_rng(22).standard_normal((B, G * H, L, D)).astype(np.float32)
+    cache = build_gpu_cache(k, v, **params)
+    qb = torch.from_numpy(q32).to("cuda").to(torch.bfloat16)
+    out = chronoquant_prefill_kernel(qb, cache, D ** -0.5, causal=causal)
+    assert out.dtype == torch.bfloat16
+    qprime = (qb.cpu() * torch.tensor(D ** -0.5, dtype=torch.bfloat16)).to(torch.float16).numpy()
+    ck, cv = build_oracle(k[0], v[0], **params)
+    ref = O.sdpa_fallback(qprime[0], ck.reconstruct(), cv.reconstruct(), 1.0, causal=causal)
+    assert_close(out.float().cpu().numpy()[0], ref.astype(np.float64), what=f"causal={causal}")
