@@ -330,6 +330,53 @@ def time_prefill(dev, stream, steps, T=8192, L=512):
     return res
 
 
+def time_e2e(dev, prompt_len=8192, n_new=512, chunk=512):
+    """random-init Qwen-style decoder (32 layers, hidden 4096, GQA
+    32/8, SwiGLU 12288, RoPE 1e6, vocab 151936, bf16 N(0, 0.02)) with
+    Full-Throttle V3 ChronoQuant caches in every layer via apply(): the
+    prompt in chunk-token prefill chunks, then n_new greedy tokens (decode
+    steps captured as one HIP graph, positions on the device)."""
+    import torch
+
+    from chronoquant_mlx_amd import create_full_throttle_caches, patch
+    from chronoquant_mlx_amd.models.qwen import ModelArgs, generate, random_model
+    args = ModelArgs()
+    model = random_model(args, device=dev, seed=0)
+    n_params = sum(p.numel() for p in model.parameters())
+    patch.apply()
+    try:
+        prompt = torch.randint(0, args.vocab_size, (1, prompt_len),
+                               generator=torch.Generator().manual_seed(0)).to(dev)
+        # warm-up on a short prompt (kernel loading, library handles, workspaces)
+        generate(model, create_full_throttle_caches(model), prompt[:, :chunk], 4, chunk)
+        caches = create_full_throttle_caches(model)
+        toks, t_pre, t_dec = generate(model, caches, prompt, n_new, chunk)
+    finally:
+        patch.revert()
+    total_tokens = prompt_len + n_new - 1
+    kv = sum(c.nbytes for c in caches)
+    fp16_kv = 2 * args.num_hidden_layers * args.num_key_value_heads * args.head_dim * 2
+    res = {"workload": f"Qwen-style decoder {args.num_hidden_layers} layers hidden "
+                       f"{args.hidden_size} GQA {args.num_attention_heads}/{args.num_key_value_heads} "
+                       f"SwiGLU {args.intermediate_size} vocab {args.vocab_size}, bf16 random "
+                       f"N(0,0.02) ({n_params / 1e9:.2f}B params); {prompt_len}-token prompt in "
+                       f"{chunk}-token chunks + {n_new} greedy tokens; Full-Throttle V3 caches",
+           "prefill_tokens_per_s": round(prompt_len / t_pre, 1),
+           "decode_tokens_per_s": round((n_new - 1) / t_dec, 2),
+           "decode_ms_per_token": round(t_dec / (n_new - 1) * 1e3, 3),
+           "end_to_end_tokens_per_s": round((prompt_len + n_new - 1) / (t_pre + t_dec), 1),
+           "kv_bytes_per_token": round(kv / total_tokens, 1),
+           "fp16_kv_bytes_per_token": fp16_kv,
+           "weight_bytes": int(sum(p.numel() * p.element_size() for p in model.parameters())),
+           "data": "uniform random token ids, seed 0"}
+    log(f"[bench] c4: prefill {res['prefill_tokens_per_s']} tok/s, decode "
+        f"{res['decode_tokens_per_s']} tok/s ({res['decode_ms_per_token']} ms/token), "
+        f"KV {res['kv_bytes_per_token']} B/token (fp16 {fp16_kv})")
+    del model, caches
+    torch.cuda.empty_cache()
+    return res
+
+
 def cpu_baseline(cfg, k, v, q, budget_s=12.0):
     from oracle import oracle as O
     threads = min(16, len(os.sched_getaffinity(0)))
@@ -364,7 +411,9 @@ def main():
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run plain 256 MiB copies (counter scale reference)")
     ap.add_argument("--no-extra", action="store_true",
-                    help="skip the supplementary ftv3_16k / c2 / c3 measurements")
+                    help="skip the supplementary ftv3_16k / c2 / c3 / prefill / c4 measurements")
+    ap.add_argument("--no-e2e", action="store_true",
+                    help="skip the end-to-end configs[4] model run")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on exactly one GPU; --gpus must be 1 "
@@ -474,6 +523,8 @@ def main():
                                          device_gen=True)
         extra["c3"] = time_streaming("c3", dev, stream)
         extra["prefill"] = time_prefill(dev, stream, 50)
+        if not args.no_e2e:
+            extra["c4"] = time_e2e(dev)
         result["extra"] = extra
 
     if not args.no_cpu_baseline:

@@ -58,7 +58,7 @@ def chronoquant_sdpa(queries: torch.Tensor, keys, values, cache, scale: float, m
     )
     if use_fused:
         q = queries.reshape(batch, n_q_heads, head_dim)
-        out = chronoquant_sdpa_kernel(q, cache, scale)
+        out = chronoquant_sdpa_kernel(q, cache, scale, seq_lens=cache._dev_len)
         return out.reshape(batch, n_q_heads, q_len, head_dim)
 
     if PREFILL_KERNEL and prefill_supported(queries, cache, mask):

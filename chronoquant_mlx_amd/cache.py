@@ -107,6 +107,8 @@ class ChronoQuantCache:
         self._pk = {"k": None, "v": None}
         self._sc = {"k": None, "v": None}
         self._max_len = 0
+        self._dev_pos = None  # device positions (bind_device_position)
+        self._dev_len = None
 
     # ------------------------------------------------------------------
     # counting (cache.py:53-61)
@@ -249,14 +251,51 @@ class ChronoQuantCache:
             keys = keys.contiguous()
         if values.stride(-1) != 1:
             values = values.contiguous()
-        self._ensure_capacity(self.offset + S)
         ks = (ctypes.c_int64 * 3)(keys.stride(0), keys.stride(1), keys.stride(2))
         vs = (ctypes.c_int64 * 3)(values.stride(0), values.stride(1), values.stride(2))
+        if self._dev_pos is not None:
+            # device positions: append at pos[b], decode reads pos[b] + S tokens
+            _lib.call("cq_append", self._descriptor(), keys.data_ptr(), ks, values.data_ptr(), vs,
+                      _lib.dtype_code(keys.dtype), S, self._dev_pos.data_ptr(), 0,
+                      _lib.stream_of(keys))
+            torch.add(self._dev_pos, S, out=self._dev_len)
+            return keys, values
+        self._ensure_capacity(self.offset + S)
         _lib.call("cq_append", self._descriptor(), keys.data_ptr(), ks, values.data_ptr(), vs,
                   _lib.dtype_code(keys.dtype), S, None, self.offset, _lib.stream_of(keys))
         self.offset += S
         self._max_len = self.offset
         return keys, values
+
+    # ------------------------------------------------------------------
+    # device positions (graph-captured serving loops; no reference counterpart)
+    # ------------------------------------------------------------------
+    def bind_device_position(self, pos: torch.Tensor | None, max_len: int = 0):
+        """Take positions from device memory instead of the host offset.
+
+        With `pos` (int32 [B], on the cache's device) bound, update_and_fetch
+        appends sequence b's new tokens at pos[b].. and the fused decode reads
+        pos[b] + S tokens.  No host value changes between steps, so a captured
+        HIP graph of a decode step replays at successive positions.  The
+        caller advances pos on the device and the host-side offset with
+        advance() after each step.  Room for max_len tokens is reserved now
+        (no reallocation may happen under capture).  pos=None returns to host
+        offsets.
+        """
+        if pos is None:
+            self._dev_pos = self._dev_len = None
+            self._max_len = self.offset
+            return
+        if pos.dtype != torch.int32 or pos.dim() != 1:
+            raise TypeError("pos must be an int32 vector [B]")
+        self.reserve(max_len)
+        self._dev_pos = pos
+        self._dev_len = torch.empty_like(pos)
+        self._max_len = int(max_len)
+
+    def advance(self, n: int):
+        """Host-side offset after n tokens were appended at device positions."""
+        self.offset += int(n)
 
     # ------------------------------------------------------------------
     # reconstruction (cache.py:131-160)

@@ -75,7 +75,9 @@ def chronoquant_sdpa_kernel(q: torch.Tensor, cache, scale: float = 1.0,
     desc = cache._descriptor()
     ws = cache._decode_workspace(nq)
     if seq_lens is not None:
-        lens = seq_lens.to(device=q.device, dtype=torch.int32).contiguous()
+        lens = seq_lens
+        if lens.device != q.device or lens.dtype != torch.int32 or not lens.is_contiguous():
+            lens = lens.to(device=q.device, dtype=torch.int32).contiguous()
         max_len = int(cache._max_len)
         lens_ptr = lens.data_ptr()
     else:

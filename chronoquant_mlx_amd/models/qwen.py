@@ -1,0 +1,266 @@
+"""Qwen-style decoder for the end-to-end run with ChronoQuant caches.
+
+The reference's end-to-end scripts drive an mlx_lm Qwen model whose
+attention modules call mlx_lm's `scaled_dot_product_attention` with the
+layer's cache; patch.apply() rebinds that symbol so ChronoQuant caches take
+the fused path (patch.py:18-33), and create_full_throttle_caches() fills the
+cache slots (patch.py:91-104).  This module is that model on PyTorch-ROCm:
+Qwen3-style blocks (RMSNorm, q/k RMSNorm per head, RoPE on half-split
+dims, SwiGLU MLP, untied LM head) whose attention calls this module's
+`scaled_dot_product_attention`, the binding apply() replaces.  Keys are
+cached after RoPE, as in mlx_lm.
+
+Dense projections are plain torch matmuls (hipBLASLt); the attention and
+the KV cache are the library's.  Weights are random N(0, 0.02) (no
+checkpoint is available offline).
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import torch
+import torch.nn.functional as F
+from torch import nn
+
+from ..host import scaled_dot_product_attention  # rebound by patch.apply()
+
+
+@dataclass
+class ModelArgs:
+    hidden_size: int = 4096
+    num_hidden_layers: int = 32
+    num_attention_heads: int = 32
+    num_key_value_heads: int = 8
+    head_dim: int = 128
+    intermediate_size: int = 12288
+    rms_norm_eps: float = 1e-6
+    rope_theta: float = 1e6
+    vocab_size: int = 151936
+    max_position: int = 40960
+
+
+class RMSNorm(nn.Module):
+    def __init__(self, dim: int, eps: float):
+        super().__init__()
+        self.weight = nn.Parameter(torch.ones(dim))
+        self.eps = eps
+
+    def forward(self, x):
+        xf = x.float()
+        y = xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + self.eps)
+        return (y * self.weight.float()).to(x.dtype)
+
+
+class Rope(nn.Module):
+    """Rotary embedding on half-split dims (non-interleaved), base theta."""
+
+    def __init__(self, dim: int, theta: float, max_position: int):
+        super().__init__()
+        inv = 1.0 / (theta ** (torch.arange(0, dim, 2, dtype=torch.float64) / dim))
+        ang = torch.arange(max_position, dtype=torch.float64)[:, None] * inv[None, :]
+        self.register_buffer("cos", torch.cos(ang).float(), persistent=False)
+        self.register_buffer("sin", torch.sin(ang).float(), persistent=False)
+
+    def forward(self, x, positions):
+        """x [B, H, L, D]; positions [L] (int64) or [B, L] on x's device."""
+        cos, sin = self.cos[positions], self.sin[positions]
+        if cos.dim() == 2:
+            cos, sin = cos[None, None], sin[None, None]
+        else:
+            cos, sin = cos[:, None], sin[:, None]
+        xf = x.float()
+        h = x.shape[-1] // 2
+        x1, x2 = xf[..., :h], xf[..., h:]
+        return torch.cat([x1 * cos - x2 * sin, x2 * cos + x1 * sin], dim=-1).to(x.dtype)
+
+
+class Attention(nn.Module):
+    def __init__(self, a: ModelArgs, rope: Rope):
+        super().__init__()
+        self.nh, self.nkv, self.hd = a.num_attention_heads, a.num_key_value_heads, a.head_dim
+        self.scale = a.head_dim ** -0.5
+        self.q_proj = nn.Linear(a.hidden_size, self.nh * self.hd, bias=False)
+        self.k_proj = nn.Linear(a.hidden_size, self.nkv * self.hd, bias=False)
+        self.v_proj = nn.Linear(a.hidden_size, self.nkv * self.hd, bias=False)
+        self.o_proj = nn.Linear(self.nh * self.hd, a.hidden_size, bias=False)
+        self.q_norm = RMSNorm(self.hd, a.rms_norm_eps)
+        self.k_norm = RMSNorm(self.hd, a.rms_norm_eps)
+        self.rope = rope
+
+    def forward(self, x, positions, mask, cache):
+        B, L, _ = x.shape
+        q = self.q_norm(self.q_proj(x).view(B, L, self.nh, self.hd)).transpose(1, 2)
+        k = self.k_norm(self.k_proj(x).view(B, L, self.nkv, self.hd)).transpose(1, 2)
+        v = self.v_proj(x).view(B, L, self.nkv, self.hd).transpose(1, 2)
+        q = self.rope(q, positions)
+        k = self.rope(k, positions)
+        keys, values = cache.update_and_fetch(k, v)
+        out = scaled_dot_product_attention(q, keys, values, cache=cache, scale=self.scale,
+                                           mask=mask)
+        return self.o_proj(out.transpose(1, 2).reshape(B, L, self.nh * self.hd))
+
+
+class MLP(nn.Module):
+    def __init__(self, a: ModelArgs):
+        super().__init__()
+        self.gate_proj = nn.Linear(a.hidden_size, a.intermediate_size, bias=False)
+        self.up_proj = nn.Linear(a.hidden_size, a.intermediate_size, bias=False)
+        self.down_proj = nn.Linear(a.intermediate_size, a.hidden_size, bias=False)
+
+    def forward(self, x):
+        return self.down_proj(F.silu(self.gate_proj(x)) * self.up_proj(x))
+
+
+class Block(nn.Module):
+    def __init__(self, a: ModelArgs, rope: Rope):
+        super().__init__()
+        self.self_attn = Attention(a, rope)
+        self.mlp = MLP(a)
+        self.input_layernorm = RMSNorm(a.hidden_size, a.rms_norm_eps)
+        self.post_attention_layernorm = RMSNorm(a.hidden_size, a.rms_norm_eps)
+
+    def forward(self, x, positions, mask, cache):
+        h = x + self.self_attn(self.input_layernorm(x), positions, mask, cache)
+        return h + self.mlp(self.post_attention_layernorm(h))
+
+
+class Model(nn.Module):
+    def __init__(self, a: ModelArgs):
+        super().__init__()
+        self.args = a
+        self.rope = Rope(a.head_dim, a.rope_theta, a.max_position)
+        self.embed_tokens = nn.Embedding(a.vocab_size, a.hidden_size)
+        self.layers = nn.ModuleList([Block(a, self.rope) for _ in range(a.num_hidden_layers)])
+        self.norm = RMSNorm(a.hidden_size, a.rms_norm_eps)
+        self.lm_head = nn.Linear(a.hidden_size, a.vocab_size, bias=False)
+
+    def forward(self, tokens, cache, positions=None, last_only: bool = False):
+        """tokens [B, L]; positions [L] (default: the caches' offset onward)
+        or [B, L] device tensor (graph-captured decode).  last_only: logits of
+        the last position only."""
+        B, L = tokens.shape
+        if positions is None:
+            off = cache[0].offset
+            positions = torch.arange(off, off + L, device=tokens.device)
+        mask = "causal" if L > 1 else None
+        x = self.embed_tokens(tokens)
+        for layer, c in zip(self.layers, cache):
+            x = layer(x, positions, mask, c)
+        if last_only:
+            x = x[:, -1:]
+        return self.lm_head(self.norm(x))
+
+
+def random_model(args: ModelArgs | None = None, device="cuda", dtype=torch.bfloat16,
+                 seed: int = 0, std: float = 0.02) -> Model:
+    """Model with every matrix drawn from N(0, std) (norm weights 1)."""
+    args = args or ModelArgs()
+    with torch.device("meta"):
+        m = Model(args).to(dtype)  # parameters materialise directly in dtype
+    m = m.to_empty(device=device)
+    g = torch.Generator(device=device)
+    g.manual_seed(seed)
+    with torch.no_grad():
+        for name, p in m.named_parameters():
+            if name.endswith("norm.weight"):
+                p.fill_(1.0)
+            else:
+                p.normal_(0.0, std, generator=g)
+    m = m.eval()
+    # the rotary tables are fp32 (the cast above applied to every buffer)
+    m.rope = Rope(args.head_dim, args.rope_theta, args.max_position).to(device)
+    for blk in m.layers:
+        blk.self_attn.rope = m.rope
+    return m
+
+
+class GraphDecoder:
+    """Greedy decode steps of `model` captured once as a HIP graph.
+
+    The caches take their positions from one device tensor (ChronoQuantCache.
+    bind_device_position), so the captured step (embedding, every layer's
+    append + fused decode attention, LM head, argmax, position advance)
+    replays unchanged at successive positions; the host only advances the
+    caches' offsets.
+    """
+
+    def __init__(self, model: Model, caches: list, batch: int, max_len: int):
+        dev = next(model.parameters()).device
+        self.model, self.caches = model, caches
+        self.pos = torch.tensor([caches[0].offset] * batch, dtype=torch.int32, device=dev)
+        self.tok = torch.zeros(batch, 1, dtype=torch.long, device=dev)
+        for c in caches:
+            c.bind_device_position(self.pos, max_len)
+        self.graph = None
+
+    def _step(self):
+        logits = self.model(self.tok, self.caches, positions=self.pos.long()[:, None])
+        nxt = logits[:, -1].argmax(-1, keepdim=True)
+        self.tok.copy_(nxt)
+        self.pos.add_(1)
+        return nxt
+
+    def capture(self, first_token: torch.Tensor):
+        """Warm up once (allocations happen outside the graph; the warm-up
+        writes the first decode position, which the first replay rewrites
+        identically), then capture one step."""
+        pos0 = self.pos.clone()
+        self.tok.copy_(first_token)
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side), torch.no_grad():
+            self._step()
+        torch.cuda.current_stream().wait_stream(side)
+        self.pos.copy_(pos0)
+        self.tok.copy_(first_token)
+        self.graph = torch.cuda.CUDAGraph()
+        with torch.no_grad(), torch.cuda.graph(self.graph):
+            self.out = self._step()
+        self.pos.copy_(pos0)
+        self.tok.copy_(first_token)
+
+    def step(self) -> torch.Tensor:
+        """One greedy token (the tensor is overwritten by the next step)."""
+        self.graph.replay()
+        for c in self.caches:
+            c.advance(1)
+        return self.out
+
+    def release(self):
+        for c in self.caches:
+            c.bind_device_position(None)
+
+
+@torch.no_grad()
+def generate(model: Model, caches: list, prompt: torch.Tensor, n_new: int,
+             prefill_chunk: int = 512, graph: bool = True):
+    """Greedy generation: the prompt in prefill_chunk-token chunks, then n_new
+    tokens.  Returns (new tokens [B, n_new], prefill seconds, decode seconds)."""
+    import time
+    B, P = prompt.shape
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    logits = None
+    for s in range(0, P, prefill_chunk):
+        logits = model(prompt[:, s:s + prefill_chunk], caches, last_only=True)
+    first = logits[:, -1].argmax(-1, keepdim=True)
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    out = [first]
+    if graph:
+        dec = GraphDecoder(model, caches, B, P + n_new)
+        dec.capture(first)
+        torch.cuda.synchronize()
+        t1 = time.perf_counter()  # capture is set-up, not decode time
+        for _ in range(n_new - 1):
+            out.append(dec.step().clone())
+        torch.cuda.synchronize()
+        dec.release()
+    else:
+        tok = first
+        for _ in range(n_new - 1):
+            tok = model(tok, caches)[:, -1].argmax(-1, keepdim=True)
+            out.append(tok)
+        torch.cuda.synchronize()
+    t2 = time.perf_counter()
+    return torch.cat(out, dim=1), t1 - t0, t2 - t1
