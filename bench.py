@@ -414,6 +414,8 @@ def main():
                     help="skip the supplementary ftv3_16k / c2 / c3 / prefill / c4 measurements")
     ap.add_argument("--no-e2e", action="store_true",
                     help="skip the end-to-end configs[4] model run")
+    ap.add_argument("--e2e-only", action="store_true",
+                    help="run only the configs[4] model and print its figures (for profiling)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on exactly one GPU; --gpus must be 1 "
@@ -428,6 +430,9 @@ def main():
 
     cfg = synth.CONFIGS[args.config]
     dev = torch.device("cuda:0")
+    if args.e2e_only:
+        print(json.dumps({"c4": time_e2e(dev)}), flush=True)
+        return
     stream = torch.cuda.Stream(dev)
     log(f"[bench] building {cfg.name} cache (T={cfg.T}, B={cfg.B})")
     cache, k, v, kt, vt = build_cache(cfg, dev)

@@ -10,9 +10,14 @@ dims, SwiGLU MLP, untied LM head) whose attention calls this module's
 `scaled_dot_product_attention`, the binding apply() replaces.  Keys are
 cached after RoPE, as in mlx_lm.
 
-Dense projections are plain torch matmuls (hipBLASLt); the attention and
-the KV cache are the library's.  Weights are random N(0, 0.02) (no
-checkpoint is available offline).
+Dense projections are plain torch matmuls (hipBLASLt), with the q/k/v and
+the gate/up projections each fused into one matrix (rows: query heads, key
+heads, value heads; gate, up).  The attention and the KV cache are the
+library's, and so are the elementwise ops when FUSED_OPS is set (the
+default): residual add + RMSNorm, the QKV split with q/k RMSNorm and RoPE,
+and the SwiGLU gate (models/fused.py).  FUSED_OPS = False runs the same
+math as torch ops, the reference the fused ops are tested against.
+Weights are random N(0, 0.02) (no checkpoint is available offline).
 """
 from __future__ import annotations
 
@@ -23,6 +28,9 @@ import torch.nn.functional as F
 from torch import nn
 
 from ..host import scaled_dot_product_attention  # rebound by patch.apply()
+from . import fused
+
+FUSED_OPS = True  # library kernels for the elementwise ops (False: torch ops)
 
 
 @dataclass
@@ -79,21 +87,29 @@ class Attention(nn.Module):
         super().__init__()
         self.nh, self.nkv, self.hd = a.num_attention_heads, a.num_key_value_heads, a.head_dim
         self.scale = a.head_dim ** -0.5
-        self.q_proj = nn.Linear(a.hidden_size, self.nh * self.hd, bias=False)
-        self.k_proj = nn.Linear(a.hidden_size, self.nkv * self.hd, bias=False)
-        self.v_proj = nn.Linear(a.hidden_size, self.nkv * self.hd, bias=False)
+        self.qkv_proj = nn.Linear(a.hidden_size, (self.nh + 2 * self.nkv) * self.hd, bias=False)
         self.o_proj = nn.Linear(self.nh * self.hd, a.hidden_size, bias=False)
         self.q_norm = RMSNorm(self.hd, a.rms_norm_eps)
         self.k_norm = RMSNorm(self.hd, a.rms_norm_eps)
         self.rope = rope
 
+    def _qkv_torch(self, qkv, positions):
+        B, L, _ = qkv.shape
+        nq, nk = self.nh * self.hd, self.nkv * self.hd
+        q = self.q_norm(qkv[..., :nq].view(B, L, self.nh, self.hd)).transpose(1, 2)
+        k = self.k_norm(qkv[..., nq:nq + nk].reshape(B, L, self.nkv, self.hd)).transpose(1, 2)
+        v = qkv[..., nq + nk:].reshape(B, L, self.nkv, self.hd).transpose(1, 2)
+        return self.rope(q, positions), self.rope(k, positions), v
+
     def forward(self, x, positions, mask, cache):
         B, L, _ = x.shape
-        q = self.q_norm(self.q_proj(x).view(B, L, self.nh, self.hd)).transpose(1, 2)
-        k = self.k_norm(self.k_proj(x).view(B, L, self.nkv, self.hd)).transpose(1, 2)
-        v = self.v_proj(x).view(B, L, self.nkv, self.hd).transpose(1, 2)
-        q = self.rope(q, positions)
-        k = self.rope(k, positions)
+        qkv = self.qkv_proj(x)
+        if FUSED_OPS:
+            q, k, v = fused.qkv_norm_rope(qkv, self.nh, self.nkv, self.q_norm.weight,
+                                          self.k_norm.weight, self.rope.cos, self.rope.sin,
+                                          positions, self.q_norm.eps)
+        else:
+            q, k, v = self._qkv_torch(qkv, positions)
         keys, values = cache.update_and_fetch(k, v)
         out = scaled_dot_product_attention(q, keys, values, cache=cache, scale=self.scale,
                                            mask=mask)
@@ -103,12 +119,15 @@ class Attention(nn.Module):
 class MLP(nn.Module):
     def __init__(self, a: ModelArgs):
         super().__init__()
-        self.gate_proj = nn.Linear(a.hidden_size, a.intermediate_size, bias=False)
-        self.up_proj = nn.Linear(a.hidden_size, a.intermediate_size, bias=False)
+        self.inter = a.intermediate_size
+        self.gate_up_proj = nn.Linear(a.hidden_size, 2 * a.intermediate_size, bias=False)
         self.down_proj = nn.Linear(a.intermediate_size, a.hidden_size, bias=False)
 
     def forward(self, x):
-        return self.down_proj(F.silu(self.gate_proj(x)) * self.up_proj(x))
+        gu = self.gate_up_proj(x)
+        if FUSED_OPS:
+            return self.down_proj(fused.silu_mul(gu))
+        return self.down_proj(F.silu(gu[..., :self.inter]) * gu[..., self.inter:])
 
 
 class Block(nn.Module):
@@ -144,11 +163,25 @@ class Model(nn.Module):
             positions = torch.arange(off, off + L, device=tokens.device)
         mask = "causal" if L > 1 else None
         x = self.embed_tokens(tokens)
-        for layer, c in zip(self.layers, cache):
-            x = layer(x, positions, mask, c)
-        if last_only:
-            x = x[:, -1:]
-        return self.lm_head(self.norm(x))
+        if not FUSED_OPS:
+            for layer, c in zip(self.layers, cache):
+                x = layer(x, positions, mask, c)
+            if last_only:
+                x = x[:, -1:]
+            return self.lm_head(self.norm(x))
+        # fused: each residual add is folded into the RMSNorm that follows it
+        eps = self.norm.eps
+        y = fused.rms_norm(x, self.layers[0].input_layernorm.weight, eps)
+        n = len(self.layers)
+        for i, (layer, c) in enumerate(zip(self.layers, cache)):
+            a = layer.self_attn(y, positions, mask, c)
+            h, y = fused.add_rms_norm(a, x, layer.post_attention_layernorm.weight, eps)
+            m = layer.mlp(y)
+            w_next = self.layers[i + 1].input_layernorm.weight if i + 1 < n else self.norm.weight
+            if last_only and i + 1 == n:
+                m, h = m[:, -1:], h[:, -1:]
+            x, y = fused.add_rms_norm(m, h, w_next, eps)
+        return self.lm_head(y)
 
 
 def random_model(args: ModelArgs | None = None, device="cuda", dtype=torch.bfloat16,

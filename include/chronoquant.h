@@ -179,6 +179,46 @@ int cq_prefill_attn(const cq_cache_desc *cache, const void *q, int32_t q_dtype,
                     int32_t n_q_heads, int64_t n_q, float scale, int32_t causal,
                     int64_t seq_len, void *out, cq_stream_t stream);
 
+/* ---- Fused elementwise ops of the end-to-end decoder ------------------
+ * No counterpart in the reference's own files: these are the roles of
+ * mlx's mx.fast.rms_norm / mx.fast.rope and mlx_lm's SwiGLU inside the
+ * mlx_lm Qwen models that the reference's end-to-end runs drive
+ * (patch.py:91-104 fills those models' cache slots).  dtype: CQ_F16,
+ * CQ_BF16 or CQ_F32 for every tensor argument except the fp32 rotary
+ * tables; math in fp32, one rounding per stored value. */
+
+/* y[r] = x[r] * rsqrt(mean(x[r]^2) + eps) * w, rows of dim elements. */
+int cq_rms_norm(const void *x, const void *w, void *y, int64_t rows, int32_t dim,
+                float eps, int32_t dtype, cq_stream_t stream);
+
+/* Residual add + RMSNorm: h_out = round(x + residual), y = RMSNorm(h_out)
+ * with weight w (the transformer block's "h = x + attn; norm(h)"). */
+int cq_add_rms_norm(const void *x, const void *residual, const void *w, void *h_out,
+                    void *y, int64_t rows, int32_t dim, float eps, int32_t dtype,
+                    cq_stream_t stream);
+
+/* Split of a fused QKV projection into the attention layout with per-head
+ * RMSNorm and rotary embedding.  qkv: [batch][seq][(n_q_heads + 2 *
+ * n_kv_heads) * head_dim] (query heads, key heads, value heads).  Query and
+ * key heads: RMSNorm with q_w / k_w ([head_dim], null for none; the
+ * normalised value is rounded to dtype), then rotary embedding on
+ * half-split dims (dims j, j + head_dim/2 rotate by the angle whose fp32
+ * cos/sin are cos_t/sin_t[pos][j], tables [max_pos][head_dim/2]).  Value
+ * heads are copied.  q_out [batch][n_q_heads][seq][head_dim], k_out/v_out
+ * [batch][n_kv_heads][seq][head_dim].  positions: int64, element (b, l) at
+ * positions[b * pos_bstride + l]; a position outside [0, max_pos) gives NaN
+ * rows instead of a read outside the tables.  head_dim 128. */
+int cq_qkv_norm_rope(const void *qkv, const void *q_w, const void *k_w, void *q_out,
+                     void *k_out, void *v_out, const float *cos_t, const float *sin_t,
+                     int64_t max_pos, const int64_t *positions, int64_t pos_bstride,
+                     int32_t batch, int64_t seq, int32_t n_q_heads, int32_t n_kv_heads,
+                     int32_t head_dim, float eps, int32_t dtype, cq_stream_t stream);
+
+/* y[r][c] = silu(gu[r][c]) * gu[r][n + c]: the SwiGLU gate over rows of a
+ * fused [gate | up] projection (2n wide); silu rounded to dtype first. */
+int cq_silu_mul(const void *gu, void *y, int64_t rows, int64_t n, int32_t dtype,
+                cq_stream_t stream);
+
 /* Static description of a status code. */
 const char *cq_status_string(int32_t status);
 
