@@ -65,6 +65,7 @@ __device__ __forceinline__ void dequant8(const DecodeArgs &a, int ci, int64_t bh
 // Portable decode kernel: lanes per token = pow2 >= W words; each lane owns
 // one 8-dim word of its token.  Exact per-token online softmax in fp32.
 __global__ __launch_bounds__(256) void decode_generic_kernel(DecodeArgs a) {
+  prefetch_args();
   const int split = blockIdx.x;
   const int h = blockIdx.y / a.n_chunks;
   const int chunk = blockIdx.y - h * a.n_chunks;

@@ -46,6 +46,25 @@ struct DecodeArgs {
   int lpt_log2;  // portable kernel: lanes per token = 1 << lpt_log2 (>= W)
 };
 
+// Kernel arguments are read through the scalar cache, which every dispatch
+// starts cold.  The compiler places each argument's load at its first use, and
+// first uses behind branches cost one dependent miss each before the first
+// vector load can issue.  Touching every 64-byte line of the argument block at
+// entry turns them into one round trip; later argument loads hit.
+__device__ __forceinline__ void prefetch_args() {
+  static_assert(sizeof(DecodeArgs) <= 256, "argument block spans more than four lines");
+  const void *p = (const void *)__builtin_amdgcn_kernarg_segment_ptr();
+  uint32_t d0, d1, d2, d3;
+  asm volatile(
+      "s_load_dword %0, %4, 0x0\n\t"
+      "s_load_dword %1, %4, 0x40\n\t"
+      "s_load_dword %2, %4, 0x80\n\t"
+      "s_load_dword %3, %4, 0xc0\n\t"
+      "s_waitcnt lgkmcnt(0)"
+      : "=s"(d0), "=s"(d1), "=s"(d2), "=s"(d3)
+      : "s"(p));
+}
+
 __device__ __forceinline__ int64_t seq_len_of(const DecodeArgs &a, int b) {
   return a.seq_lens ? min((int64_t)max(a.seq_lens[b], 0), a.max_T) : a.seq_len;
 }
@@ -107,66 +126,18 @@ __device__ __forceinline__ void store_dev1(__amdgpu_buffer_rsrc_t r, uint32_t of
   __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(int, v), r, (int)off, 0, kPolicyDevice);
 }
 
-// Per-workgroup epilogue.  The workgroup's merged state for q heads
-// j0 .. j0+gn-1 of kv head h is in LDS: wm[j] (running max, log2 units),
-// wl[j] (sum of weights), wo[j*ostride + d] (unnormalised output).  With one
-// split it writes the output; otherwise it writes a partial, and the last
-// workgroup of (b, h, chunk) to finish merges all partials and resets the
-// counter it used.
-//
-// The merge costs one memory round trip: a thread owns (head, 4 dims) and a
-// slice of the splits, issues every load of its splits ((m, l) pairs and
-// 16-byte partial vectors) before using any, folds them with a running
-// log-sum-exp, and the slices of a unit (adjacent lanes) are folded the same
-// way with xor shuffles.
 constexpr int kCombineBatch = 8;  // splits whose loads are in flight together
 
-__device__ __forceinline__ void finish_workgroup(const DecodeArgs &a, int b, int h, int chunk,
-                                                 int j0, int gn, int split, const float *wm,
-                                                 const float *wl, const float *wo,
-                                                 int ostride) {
+// The last workgroup's fold of the nsplit partials of every (head, 4 dims).
+// A unit's `slices` threads are adjacent lanes (slices a power of two <= 64),
+// so the slices fold with xor shuffles: no LDS, no barrier.  The batch loop is
+// fully unrolled and branch-free, so all of a batch's loads are in flight
+// together (a branch inside it would make the compiler wait for each load).
+template <bool Vec>
+__device__ __forceinline__ void merge_partials(const DecodeArgs &a, __amdgpu_buffer_rsrc_t racc,
+                                               __amdgpu_buffer_rsrc_t rml, int64_t bq0, int gn) {
   const int tid = threadIdx.x, nthr = blockDim.x;
-  const int D = a.D, nd4 = (D + 3) / 4;
-  const bool vec = (D & 3) == 0;  // 16-byte partial accesses
-  const int64_t bq0 = (int64_t)b * a.nq + h * a.G + j0;
-  if (a.nsplit == 1) {
-    for (int e = tid; e < gn * D; e += nthr) {
-      const int j = e / D, dim = e - j * D;
-      const float L = wl[j], O = wo[j * ostride + dim];
-      store_any(a.out_dtype, a.out, (bq0 + j) * D + dim, L > 0.f ? O / L : 0.f);
-    }
-    return;
-  }
-  const int nsplit = a.nsplit;
-  // partials: (m, l) and o of this split, 16 bytes per access
-  for (int u = tid; u < gn * nd4; u += nthr) {
-    const int j = u / nd4, d0 = 4 * (u - j * nd4);
-    const int64_t row = (bq0 + j) * nsplit + split;
-    const __amdgpu_buffer_rsrc_t racc = make_rsrc(a.part_acc + row * D, (uint32_t)D * 4u);
-    const float *o = wo + j * ostride + d0;
-    if (vec) {
-      store_dev4(racc, 4u * d0, f4v_t{o[0], o[1], o[2], o[3]});
-    } else {
-      for (int c = 0; c < 4 && d0 + c < D; ++c) store_dev1(racc, 4u * (d0 + c), o[c]);
-    }
-    if (d0 == 0) store_dev2(make_rsrc(a.part_ml + row * 2, 8u), 0u, f2v_t{wm[j], wl[j]});
-  }
-
-  __shared__ int s_last;
-  __builtin_amdgcn_s_waitcnt(0);  // this thread's partial stores are complete
-  __syncthreads();
-  uint32_t *ctr = a.counters + ((int64_t)b * a.H + h) * a.n_chunks + chunk;
-  if (tid == 0) {
-    const uint32_t prev =
-        __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    s_last = (prev == (uint32_t)(nsplit - 1));
-  }
-  __syncthreads();
-  if (!s_last) return;
-
-  // ---- last workgroup: fold the nsplit partials of every (head, 4 dims) ----
-  // A unit's `slices` threads are adjacent lanes (slices a power of two <= 64),
-  // so the slices fold with xor shuffles: no LDS, no barrier.
+  const int D = a.D, nd4 = (D + 3) / 4, nsplit = a.nsplit;
   const int units = gn * nd4;
   int slices = 1;
   while (slices * 2 <= nsplit && units * slices * 2 <= nthr && slices < 64) slices *= 2;
@@ -177,10 +148,7 @@ __device__ __forceinline__ void finish_workgroup(const DecodeArgs &a, int b, int
     const bool live = u < units;  // whole slice groups are live together
     const int uu = live ? u : 0;
     const int j = uu / nd4, d0 = 4 * (uu - j * nd4);
-    const int64_t row0 = (bq0 + j) * nsplit;
-    const __amdgpu_buffer_rsrc_t rml = make_rsrc(a.part_ml + row0 * 2, (uint32_t)nsplit * 8u);
-    const __amdgpu_buffer_rsrc_t racc =
-        make_rsrc(a.part_acc + row0 * D, (uint32_t)nsplit * (uint32_t)D * 4u);
+    const uint32_t row0 = (uint32_t)((bq0 + j) * nsplit);
     float M = -INFINITY, L = 0.f;
     float o[4] = {0.f, 0.f, 0.f, 0.f};
     for (int sp0 = sl; sp0 < nsplit; sp0 += kCombineBatch * slices) {
@@ -188,16 +156,17 @@ __device__ __forceinline__ void finish_workgroup(const DecodeArgs &a, int b, int
       f4v_t ov[kCombineBatch];
 #pragma unroll
       for (int k = 0; k < kCombineBatch; ++k) {
-        // splits past the end read past the buffer (zeros) and are masked below
-        const uint32_t spo = (uint32_t)min(sp0 + k * slices, nsplit);
+        // splits past the end read the next row or past the buffer (zeros);
+        // they are masked below
+        const uint32_t spo = row0 + (uint32_t)min(sp0 + k * slices, nsplit);
         ml[k] = load_dev2(rml, spo * 8u);
         const uint32_t off = (spo * (uint32_t)D + (uint32_t)d0) * 4u;
-        if (vec) {
+        if constexpr (Vec) {
           ov[k] = load_dev4(racc, off);
         } else {
-          ov[k] = f4v_t{load_dev1(racc, off), d0 + 1 < D ? load_dev1(racc, off + 4u) : 0.f,
-                        d0 + 2 < D ? load_dev1(racc, off + 8u) : 0.f,
-                        d0 + 3 < D ? load_dev1(racc, off + 12u) : 0.f};
+          // dims past D read the next row (or zeros past the buffer): unused
+          ov[k] = f4v_t{load_dev1(racc, off), load_dev1(racc, off + 4u), load_dev1(racc, off + 8u),
+                        load_dev1(racc, off + 12u)};
         }
       }
       float mb = M;
@@ -206,14 +175,17 @@ __device__ __forceinline__ void finish_workgroup(const DecodeArgs &a, int b, int
         if (sp0 + k * slices >= nsplit) ml[k].x = -INFINITY;
         mb = fmaxf(mb, ml[k].x);
       }
-      if (mb == -INFINITY) continue;
-      const float f = (M == -INFINITY) ? 0.f : fast_exp2(M - mb);
+      // no branch on mb: a branch would let the compiler sink the partial
+      // loads below it, a second round trip.  mb = -inf (nothing yet) gives
+      // zero factors and weights.
+      const float mref = (mb == -INFINITY) ? 0.f : mb;
+      const float f = (M == -INFINITY) ? 0.f : fast_exp2(M - mref);
       L *= f;
 #pragma unroll
       for (int c = 0; c < 4; ++c) o[c] *= f;
 #pragma unroll
       for (int k = 0; k < kCombineBatch; ++k) {
-        const float w = (ml[k].x == -INFINITY) ? 0.f : fast_exp2(ml[k].x - mb);
+        const float w = (ml[k].x == -INFINITY) ? 0.f : fast_exp2(ml[k].x - mref);
         L += w * ml[k].y;
         o[0] += w * ov[k].x;
         o[1] += w * ov[k].y;
@@ -237,7 +209,7 @@ __device__ __forceinline__ void finish_workgroup(const DecodeArgs &a, int b, int
     if (live && sl == 0) {
       const float inv = L > 0.f ? 1.f / L : 0.f;
       const int64_t oi = (bq0 + j) * D + d0;
-      if (a.out_dtype == CQ_F16 && vec) {
+      if (Vec && a.out_dtype == CQ_F16) {
         const h2v_t lo = h2v_t{(_Float16)(o[0] * inv), (_Float16)(o[1] * inv)};
         const h2v_t hi = h2v_t{(_Float16)(o[2] * inv), (_Float16)(o[3] * inv)};
         *(uint2 *)((uint16_t *)a.out + oi) =
@@ -247,6 +219,73 @@ __device__ __forceinline__ void finish_workgroup(const DecodeArgs &a, int b, int
       }
     }
   }
+}
+
+// Per-workgroup epilogue.  The workgroup's merged state for q heads
+// j0 .. j0+gn-1 of kv head h is in LDS: wm[j] (running max, log2 units),
+// wl[j] (sum of weights), wo[j*ostride + d] (unnormalised output).  With one
+// split it writes the output; otherwise it writes a partial, and the last
+// workgroup of (b, h, chunk) to finish merges all partials and resets the
+// counter it used.
+//
+// The merge costs one memory round trip: a thread owns (head, 4 dims) and a
+// slice of the splits, issues every load of its splits ((m, l) pairs and
+// 16-byte partial vectors) before using any, folds them with a running
+// log-sum-exp, and the slices of a unit (adjacent lanes) are folded the same
+// way with xor shuffles.
+
+__device__ __forceinline__ void finish_workgroup(const DecodeArgs &a, int b, int h, int chunk,
+                                                 int j0, int gn, int split, const float *wm,
+                                                 const float *wl, const float *wo,
+                                                 int ostride) {
+  const int tid = threadIdx.x, nthr = blockDim.x;
+  const int D = a.D, nd4 = (D + 3) / 4;
+  const bool vec = (D & 3) == 0;  // 16-byte partial accesses
+  const int64_t bq0 = (int64_t)b * a.nq + h * a.G + j0;
+  if (a.nsplit == 1) {
+    for (int e = tid; e < gn * D; e += nthr) {
+      const int j = e / D, dim = e - j * D;
+      const float L = wl[j], O = wo[j * ostride + dim];
+      store_any(a.out_dtype, a.out, (bq0 + j) * D + dim, L > 0.f ? O / L : 0.f);
+    }
+    return;
+  }
+  const int nsplit = a.nsplit;
+  // One wave-uniform buffer resource per partial array (32-bit offsets: the
+  // host bounds both arrays below 2^31 bytes).  Per-lane resources would make
+  // the compiler serialise every access over the distinct resources.
+  const uint32_t rows = (uint32_t)(a.B * a.nq * nsplit);
+  const __amdgpu_buffer_rsrc_t racc = make_rsrc(a.part_acc, rows * (uint32_t)D * 4u);
+  const __amdgpu_buffer_rsrc_t rml = make_rsrc(a.part_ml, rows * 8u);
+  // partials: (m, l) and o of this split, 16 bytes per access
+  for (int u = tid; u < gn * nd4; u += nthr) {
+    const int j = u / nd4, d0 = 4 * (u - j * nd4);
+    const uint32_t row = (uint32_t)((bq0 + j) * nsplit + split);
+    const uint32_t base = row * (uint32_t)D * 4u;
+    const float *o = wo + j * ostride + d0;
+    if (vec) {
+      store_dev4(racc, base + 4u * d0, f4v_t{o[0], o[1], o[2], o[3]});
+    } else {
+      for (int c = 0; c < 4 && d0 + c < D; ++c) store_dev1(racc, base + 4u * (d0 + c), o[c]);
+    }
+    if (d0 == 0) store_dev2(rml, row * 8u, f2v_t{wm[j], wl[j]});
+  }
+
+  __shared__ int s_last;
+  __builtin_amdgcn_s_waitcnt(0);  // this thread's partial stores are complete
+  __syncthreads();
+  uint32_t *ctr = a.counters + ((int64_t)b * a.H + h) * a.n_chunks + chunk;
+  if (tid == 0) {
+    const uint32_t prev =
+        __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    s_last = (prev == (uint32_t)(nsplit - 1));
+  }
+  __syncthreads();
+  if (!s_last) return;
+
+  // ---- last workgroup: fold the nsplit partials of every (head, 4 dims) ----
+  if (vec) merge_partials<true>(a, racc, rml, bq0, gn);
+  else merge_partials<false>(a, racc, rml, bq0, gn);
   if (tid == 0) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
@@ -328,6 +367,8 @@ inline int prepare_launch(DecodeArgs &a, int chunk_heads, int64_t resident, void
   a.split_len = p.split_len;
   if (a.nsplit > 1) {
     if ((int64_t)a.B * a.H * a.n_chunks > kMaxCounters) return CQ_ERR_UNSUPPORTED;
+    // the split partials are addressed with 32-bit byte offsets
+    if ((int64_t)a.B * a.nq * a.nsplit * a.D * 4 >= ((int64_t)1 << 31)) return CQ_ERR_UNSUPPORTED;
     if (!workspace) return CQ_ERR_WORKSPACE;
     if ((uintptr_t)workspace & 255) return CQ_ERR_ALIGN;
     if (ws_bytes < workspace_bytes_for(a.B, a.nq, a.D, a.nsplit)) return CQ_ERR_WORKSPACE;

@@ -97,15 +97,19 @@ __device__ __forceinline__ uint32_t and_or(uint32_t x, uint32_t m, uint32_t o) {
   return (x & m) | o;
 }
 
+// Cache-stream loads: every cache byte is read once per decode, so they are
+// non-temporal (cache policy nt) and do not evict the kernel's code, the
+// argument block or the split partials from L2.
+constexpr int kPolicyStream = 2;
 __device__ __forceinline__ uint32_t bload32(__amdgpu_buffer_rsrc_t r, uint32_t off) {
-  return (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(r, (int)off, 0, 0);
+  return (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(r, (int)off, 0, kPolicyStream);
 }
 __device__ __forceinline__ uint4 bload128(__amdgpu_buffer_rsrc_t r, uint32_t off) {
-  const i4_t v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0);
+  const i4_t v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, kPolicyStream);
   return uint4{(uint32_t)v[0], (uint32_t)v[1], (uint32_t)v[2], (uint32_t)v[3]};
 }
 __device__ __forceinline__ uint32_t bload16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
-  return (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(r, (int)off, 0, 0);
+  return (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(r, (int)off, 0, kPolicyStream);
 }
 
 __device__ __forceinline__ f4_t mfma32(h8_t a, h8_t b, f4_t c) {
@@ -255,6 +259,7 @@ __device__ __forceinline__ void merge_and_finish(const DecodeArgs &a, DecodeLds 
 template <bool Pow2>
 __global__ __launch_bounds__(kThreadsMfma) void decode_mfma_kernel(DecodeArgs a) {
   __shared__ DecodeLds lds;
+  prefetch_args();
   const int split = blockIdx.x;
   const int h = blockIdx.y / a.n_chunks;
   const int chunk = blockIdx.y - h * a.n_chunks;
@@ -583,6 +588,7 @@ __global__ __launch_bounds__(kThreadsMfma) void decode_mfma_kernel(DecodeArgs a)
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(kThreadsMfma) void decode_plain_kernel(DecodeArgs a) {
   __shared__ DecodeLds lds;
+  prefetch_args();
   const int split = blockIdx.x;
   const int h = blockIdx.y / a.n_chunks;
   const int chunk = blockIdx.y - h * a.n_chunks;
