@@ -300,7 +300,7 @@ struct SplitPlan {
 // Workgroups of `kernel` (launched with `threads` threads) that run at once on
 // the current device: CUs x maximum active blocks per CU, cached per device
 // under `slot` (one slot per decode kernel).
-enum ResidentSlot { kSlotGeneric = 0, kSlotMfmaPow2, kSlotMfma, kSlotPlain, kSlotCount };
+enum ResidentSlot { kSlotGeneric = 0, kSlotMfmaPow2, kSlotMfma, kSlotPlain, kSlotG4, kSlotCount };
 int64_t resident_workgroups(const void *kernel, int threads, int slot);
 int64_t mfma_max_resident();     // max over the MFMA-file kernels
 int64_t decode_max_resident();   // max over every decode kernel
@@ -382,5 +382,9 @@ inline int prepare_launch(DecodeArgs &a, int chunk_heads, int64_t resident, void
 
 int launch_decode_mfma(DecodeArgs &a, void *workspace, size_t ws_bytes, hipStream_t stream);
 bool mfma_supported(const DecodeArgs &a);
+// GQA groups of at most 4 q heads (cq_decode_g4.hip)
+bool g4_supported(const DecodeArgs &a);
+int64_t g4_resident();
+int launch_decode_g4(DecodeArgs &a, void *workspace, size_t ws_bytes, hipStream_t stream);
 
 }  // namespace cq
