@@ -45,13 +45,16 @@ struct alignas(16) G4WaveScratch {
   int slot_v[kChunk];            // V P-frame slot per token (-1: I-frame / padding)
   uint32_t s16[2][kChunk];       // fp16 K scale | fp16 V scale << 16 (0: none)
   float qa[16][kG4];             // log2e * q'.anchor_k - mref by (local anchor, head)
-  uint2 pw[3][kG4][kChunk / 4];  // p, p*s_v, p*s_v/16 (fp16) by (head, 4-token group)
+  // p, p*s_v, p*s_v/16 (fp16) by (head, 4-token group); rows padded to 34
+  // dwords so the 4 heads of a 4-token group fall in different banks
+  uint2 pw[3][kG4][kChunk / 4 + 1];
 };
 
 // Per-workgroup LDS: q' of the group's heads in the unpack order of each
 // 8-dim slab, and the zero region the score product's off-block lanes read.
 struct alignas(16) G4GroupScratch {
   h8_t q[16][kG4];
+  h8_t pad[kG4];  // puts zero[m][h] 64 bytes off q[m][h]'s banks
   h8_t zero[16][kG4];
   float s8[kG4];  // 8 * sum_d q'_d per head
 };
