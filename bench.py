@@ -138,13 +138,13 @@ def copy_calibration(dev, nbytes=256 << 20, reps=4):
     log(f"[bench] copy calibration: {reps} copies of {nbytes} bytes")
 
 
-TRAFFIC_FILE = os.path.join(ROOT, "profiles", "decode_mfma_c1_traffic.txt")
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "decode_g4_c1_traffic.txt")
 
 
 def kernel_source_hash():
     import hashlib
     h = hashlib.sha256()
-    for f in ("cq_decode_mfma.hip", "cq_decode_common.h"):
+    for f in ("cq_decode_g4.hip", "cq_mfma_common.h", "cq_decode_common.h"):
         with open(os.path.join(ROOT, "chronoquant_mlx_amd", "csrc", f), "rb") as fh:
             h.update(fh.read())
     return h.hexdigest()[:16]
