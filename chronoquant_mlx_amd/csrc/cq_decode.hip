@@ -81,6 +81,7 @@ __global__ __launch_bounds__(256) void decode_generic_kernel(DecodeArgs a) {
   const int64_t T = seq_len_of(a, b);
   const int64_t t0 = (int64_t)split * a.split_len;
   const int64_t t1 = min(T, t0 + a.split_len);
+  if (split_is_empty(split, t0, T)) return;
   const bool wok = w < a.W;
 
   // q' = round_qdtype(q * round_qdtype(scale)) (attention.py:46)

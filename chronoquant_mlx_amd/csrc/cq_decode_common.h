@@ -69,6 +69,13 @@ __device__ __forceinline__ int64_t seq_len_of(const DecodeArgs &a, int b) {
   return a.seq_lens ? min((int64_t)max(a.seq_lens[b], 0), a.max_T) : a.seq_len;
 }
 
+// A split past its sequence's end has nothing to do and takes no part in the
+// combine (finish_workgroup counts only splits below the end; split 0 always
+// takes part).  Called by a whole workgroup before any barrier.
+__device__ __forceinline__ bool split_is_empty(int split, int64_t t0, int64_t T) {
+  return split > 0 && t0 >= T;
+}
+
 // t / s for 0 <= t < 2^24 and s >= 1: float estimate, then one correction
 // each way (the estimate is off by at most one).
 __device__ __forceinline__ int div_stride(int t, int s, float inv_s) {
@@ -135,9 +142,10 @@ constexpr int kCombineBatch = 8;  // splits whose loads are in flight together
 // together (a branch inside it would make the compiler wait for each load).
 template <bool Vec>
 __device__ __forceinline__ void merge_partials(const DecodeArgs &a, __amdgpu_buffer_rsrc_t racc,
-                                               __amdgpu_buffer_rsrc_t rml, int64_t bq0, int gn) {
+                                               __amdgpu_buffer_rsrc_t rml, int64_t bq0, int gn,
+                                               int nsplit) {
   const int tid = threadIdx.x, nthr = blockDim.x;
-  const int D = a.D, nd4 = (D + 3) / 4, nsplit = a.nsplit;
+  const int D = a.D, nd4 = (D + 3) / 4;
   const int units = gn * nd4;
   int slices = 1;
   while (slices * 2 <= nsplit && units * slices * 2 <= nthr && slices < 64) slices *= 2;
@@ -148,7 +156,7 @@ __device__ __forceinline__ void merge_partials(const DecodeArgs &a, __amdgpu_buf
     const bool live = u < units;  // whole slice groups are live together
     const int uu = live ? u : 0;
     const int j = uu / nd4, d0 = 4 * (uu - j * nd4);
-    const uint32_t row0 = (uint32_t)((bq0 + j) * nsplit);
+    const uint32_t row0 = (uint32_t)((bq0 + j) * a.nsplit);  // rows hold a.nsplit slots
     float M = -INFINITY, L = 0.f;
     float o[4] = {0.f, 0.f, 0.f, 0.f};
     for (int sp0 = sl; sp0 < nsplit; sp0 += kCombineBatch * slices) {
@@ -156,9 +164,9 @@ __device__ __forceinline__ void merge_partials(const DecodeArgs &a, __amdgpu_buf
       f4v_t ov[kCombineBatch];
 #pragma unroll
       for (int k = 0; k < kCombineBatch; ++k) {
-        // splits past the end read the next row or past the buffer (zeros);
-        // they are masked below
-        const uint32_t spo = row0 + (uint32_t)min(sp0 + k * slices, nsplit);
+        // splits past the end re-read the last live split (written by this
+        // call) and are masked below
+        const uint32_t spo = row0 + (uint32_t)min(sp0 + k * slices, nsplit - 1);
         ml[k] = load_dev2(rml, spo * 8u);
         const uint32_t off = (spo * (uint32_t)D + (uint32_t)d0) * 4u;
         if constexpr (Vec) {
@@ -271,6 +279,11 @@ __device__ __forceinline__ void finish_workgroup(const DecodeArgs &a, int b, int
     if (d0 == 0) store_dev2(rml, row * 8u, f2v_t{wm[j], wl[j]});
   }
 
+  // Splits holding tokens of this sequence (a shorter sequence of a ragged
+  // batch leaves the later splits empty; their workgroups exit at once and
+  // take no ticket).  Split 0 also answers an empty sequence.
+  const int64_t T = seq_len_of(a, b);
+  const int live = (int)max((int64_t)1, min((int64_t)nsplit, (T + a.split_len - 1) / a.split_len));
   __shared__ int s_last;
   __builtin_amdgcn_s_waitcnt(0);  // this thread's partial stores are complete
   __syncthreads();
@@ -278,14 +291,14 @@ __device__ __forceinline__ void finish_workgroup(const DecodeArgs &a, int b, int
   if (tid == 0) {
     const uint32_t prev =
         __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    s_last = (prev == (uint32_t)(nsplit - 1));
+    s_last = (prev == (uint32_t)(live - 1));
   }
   __syncthreads();
   if (!s_last) return;
 
   // ---- last workgroup: fold the nsplit partials of every (head, 4 dims) ----
-  if (vec) merge_partials<true>(a, racc, rml, bq0, gn);
-  else merge_partials<false>(a, racc, rml, bq0, gn);
+  if (vec) merge_partials<true>(a, racc, rml, bq0, gn, live);
+  else merge_partials<false>(a, racc, rml, bq0, gn, live);
   if (tid == 0) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 

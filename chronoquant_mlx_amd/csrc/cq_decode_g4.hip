@@ -95,6 +95,7 @@ __global__ __launch_bounds__(kThreadsMfma) void decode_g4_kernel(DecodeArgs a) {
   const int64_t T = seq_len_of(a, b);
   const int64_t t0 = (int64_t)split * a.split_len;
   const int64_t t1 = min(T, t0 + a.split_len);
+  if (split_is_empty(split, t0, T)) return;
   const int lsk = __builtin_ctz(a.stride[0]), lsv = __builtin_ctz(a.stride[1]);
   const int mk = a.stride[0] - 1, mv = a.stride[1] - 1;
 

@@ -86,6 +86,7 @@ __global__ __launch_bounds__(kThreadsMfma) void decode_mfma_kernel(DecodeArgs a)
   const int64_t T = seq_len_of(a, b);
   const int64_t t0 = (int64_t)split * a.split_len;
   const int64_t t1 = min(T, t0 + a.split_len);
+  if (split_is_empty(split, t0, T)) return;
   const int sk = a.stride[0], sv = a.stride[1];
   const float isk = a.inv_stride[0], isv = a.inv_stride[1];
   const int lsk = Pow2 ? __builtin_ctz(sk) : 0, lsv = Pow2 ? __builtin_ctz(sv) : 0;
@@ -414,6 +415,7 @@ __global__ __launch_bounds__(kThreadsMfma) void decode_plain_kernel(DecodeArgs a
   const int64_t T = seq_len_of(a, b);
   const int64_t t0 = (int64_t)split * a.split_len;
   const int64_t t1 = min(T, t0 + a.split_len);
+  if (split_is_empty(split, t0, T)) return;
   const __amdgpu_buffer_rsrc_t r_k =
       make_rsrc(a.kf[0] + bh * a.cap_kf[0] * kD, (uint32_t)(a.cap_kf[0] * kD * 2));
   const __amdgpu_buffer_rsrc_t r_v =

@@ -128,9 +128,14 @@ def test_workspace_shared_across_shapes():
                 assert_tight(out[b], O.sdpa_fused(q[b], ck, cv, D ** -0.5), what=f"T={k.shape[2]}")
 
 
-def test_ragged_lengths():
+@pytest.mark.parametrize("generic", [False, True])
+@pytest.mark.parametrize("lens", [[2000, 1, 1057, 640], [0, 2000, 513, 512], [511, 1, 2000, 0]])
+def test_ragged_lengths(generic, lens):
     # per-sequence lengths: sequence b reads only its first L_b tokens and
-    # must equal an independent cache of length L_b
+    # must equal an independent cache of length L_b.  The split plan follows
+    # the longest length (4 splits of 512 here), so shorter sequences leave
+    # later splits empty: those workgroups exit and the combine counts only
+    # the live ones.  An empty sequence answers zeros.
     rng = np.random.default_rng(21)
     B, H, T, D, G = 4, 8, 2000, 128, 4
     k = np.cumsum(rng.standard_normal((B, H, T, D)) * 0.1, axis=2).astype(np.float16)
@@ -138,13 +143,18 @@ def test_ragged_lengths():
     q = rng.standard_normal((B, G * H, D)).astype(np.float16)
     params = dict(stride_k=32, stride_v=8)
     cache = build_gpu_cache(k, v, **params)
-    lens = [2000, 1, 1057, 640]
     scale = D ** -0.5
-    out = decode_gpu(cache, q, scale, seq_lens=lens)
-    for b, L in enumerate(lens):
-        ck, cv = build_oracle(k[b, :, :L], v[b, :, :L], **params)
-        assert_close(out[b], oracle_fallback(ck, cv, q[b], scale), what=f"b={b} L={L}")
-        assert_tight(out[b], O.sdpa_fused(q[b], ck, cv, scale), what=f"b={b} L={L}")
+    # twice: the second call reuses the workspace and counters of the first
+    for _ in range(2):
+        out = decode_gpu(cache, q, scale, seq_lens=lens, generic=generic)
+        for b, L in enumerate(lens):
+            if L == 0:
+                assert np.array_equal(out[b], np.zeros_like(out[b])), f"b={b} L=0"
+                continue
+            ck, cv = build_oracle(k[b, :, :L], v[b, :, :L], **params)
+            assert_close(out[b], oracle_fallback(ck, cv, q[b], scale), what=f"b={b} L={L}")
+            assert_tight(out[b], O.sdpa_fused(q[b], ck, cv, scale), what=f"b={b} L={L}",
+                         mfma=not generic)
 
 
 def test_output_dtypes_and_fp32_queries():
