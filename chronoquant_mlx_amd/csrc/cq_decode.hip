@@ -200,7 +200,8 @@ __global__ __launch_bounds__(256) void decode_generic_kernel(DecodeArgs a) {
     s_acc[0][j][dim] = O;  // each (j, dim) is read and rewritten by one thread
   }
   __syncthreads();
-  finish_workgroup(a, b, h, chunk, j0, gn, split, w_m, w_l, &s_acc[0][0][0], kMaxHeadDim);
+  finish_workgroup(a, b, h, chunk, j0, gn, split, grid_live(a, T), w_m, w_l, &s_acc[0][0][0],
+                   kMaxHeadDim);
 }
 
 // ---------------------------------------------------------------------------
@@ -313,8 +314,12 @@ extern "C" {
 size_t cq_decode_workspace_size(int32_t batch, int32_t n_kv_heads, int32_t n_q_heads,
                                 int32_t head_dim, int64_t max_seq_len) {
   if (batch < 1 || n_kv_heads < 1 || n_q_heads < 1 || head_dim < 1) return 0;
+  // enough for the grid plan of every decode kernel and for the balanced
+  // plan of the GQA-4 kernel
   const SplitPlan p = plan_splits((int64_t)batch * n_kv_heads, max_seq_len, decode_max_resident());
-  return workspace_bytes_for(batch, n_q_heads, head_dim, p.nsplit);
+  const int64_t bal = balanced_slots(std::max((int64_t)1, decode_max_resident() / n_kv_heads),
+                                     max_seq_len);
+  return workspace_bytes_for(batch, n_q_heads, head_dim, (int)std::max((int64_t)p.nsplit, bal));
 }
 
 int cq_decode_attn_generic(const cq_cache_desc *cache, const void *q, int32_t q_dtype,

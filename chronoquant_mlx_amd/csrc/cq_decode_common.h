@@ -10,6 +10,7 @@
 #include <math.h>
 
 #include "cq_device.h"
+#include "cq_plan.h"
 
 namespace cq {
 
@@ -69,11 +70,39 @@ __device__ __forceinline__ int64_t seq_len_of(const DecodeArgs &a, int b) {
   return a.seq_lens ? min((int64_t)max(a.seq_lens[b], 0), a.max_T) : a.seq_len;
 }
 
-// A split past its sequence's end has nothing to do and takes no part in the
-// combine (finish_workgroup counts only splits below the end; split 0 always
-// takes part).  Called by a whole workgroup before any barrier.
+// Grid plan (one split of split_len tokens per workgroup, grid x): a split
+// past its sequence's end has nothing to do and takes no part in the combine;
+// split 0 always takes part.  Called by a whole workgroup before any barrier.
 __device__ __forceinline__ bool split_is_empty(int split, int64_t t0, int64_t T) {
   return split > 0 && t0 >= T;
+}
+// Grid plan: splits holding tokens of a sequence of length T (at least 1:
+// split 0 answers an empty sequence).
+__device__ __forceinline__ int grid_live(const DecodeArgs &a, int64_t T) {
+  return (int)max((int64_t)1, min((int64_t)a.nsplit, (T + a.split_len - 1) / a.split_len));
+}
+
+// Balanced plan (cq_plan.h): start[b] = first unit of sequence b, start[B] =
+// total units, for per-sequence lengths.  Wave 0 scans 64 sequences at a
+// time; the whole workgroup syncs once.
+__device__ __forceinline__ void build_unit_table(const DecodeArgs &a, int32_t *start) {
+  const int tid = threadIdx.x;
+  if (tid < 64) {
+    int32_t carry = 0;
+    for (int b0 = 0; b0 < a.B; b0 += 64) {
+      const int b = b0 + tid;
+      int32_t n = b < a.B ? (int32_t)units_of(seq_len_of(a, b)) : 0;
+#pragma unroll
+      for (int d = 1; d < 64; d *= 2) {
+        const int32_t y = __shfl_up(n, d, 64);
+        if (tid >= d) n += y;
+      }
+      if (b < a.B) start[b + 1] = carry + n;
+      carry += __shfl(n, 63, 64);
+    }
+    if (tid == 0) start[0] = 0;
+  }
+  __syncthreads();
 }
 
 // t / s for 0 <= t < 2^24 and s >= 1: float estimate, then one correction
@@ -144,7 +173,7 @@ template <bool Vec>
 __device__ __forceinline__ void merge_partials(const DecodeArgs &a, __amdgpu_buffer_rsrc_t racc,
                                                __amdgpu_buffer_rsrc_t rml, int64_t bq0, int gn,
                                                int nsplit) {
-  const int tid = threadIdx.x, nthr = blockDim.x;
+  const int tid = thread_id(), nthr = blockDim.x;
   const int D = a.D, nd4 = (D + 3) / 4;
   const int units = gn * nd4;
   int slices = 1;
@@ -231,10 +260,11 @@ __device__ __forceinline__ void merge_partials(const DecodeArgs &a, __amdgpu_buf
 
 // Per-workgroup epilogue.  The workgroup's merged state for q heads
 // j0 .. j0+gn-1 of kv head h is in LDS: wm[j] (running max, log2 units),
-// wl[j] (sum of weights), wo[j*ostride + d] (unnormalised output).  With one
-// split it writes the output; otherwise it writes a partial, and the last
-// workgroup of (b, h, chunk) to finish merges all partials and resets the
-// counter it used.
+// wl[j] (sum of weights), wo[j*ostride + d] (unnormalised output).  `live`
+// workgroups share sequence b; this one holds partial slot `slot`.  With
+// live == 1 it writes the output; otherwise it writes its partial, and the
+// last of the live workgroups of (b, h, chunk) to finish merges all partials
+// and resets the counter it used.
 //
 // The merge costs one memory round trip: a thread owns (head, 4 dims) and a
 // slice of the splits, issues every load of its splits ((m, l) pairs and
@@ -243,14 +273,14 @@ __device__ __forceinline__ void merge_partials(const DecodeArgs &a, __amdgpu_buf
 // way with xor shuffles.
 
 __device__ __forceinline__ void finish_workgroup(const DecodeArgs &a, int b, int h, int chunk,
-                                                 int j0, int gn, int split, const float *wm,
-                                                 const float *wl, const float *wo,
-                                                 int ostride) {
-  const int tid = threadIdx.x, nthr = blockDim.x;
+                                                 int j0, int gn, int slot, int live,
+                                                 const float *wm, const float *wl,
+                                                 const float *wo, int ostride) {
+  const int tid = thread_id(), nthr = blockDim.x;
   const int D = a.D, nd4 = (D + 3) / 4;
   const bool vec = (D & 3) == 0;  // 16-byte partial accesses
   const int64_t bq0 = (int64_t)b * a.nq + h * a.G + j0;
-  if (a.nsplit == 1) {
+  if (live == 1) {
     for (int e = tid; e < gn * D; e += nthr) {
       const int j = e / D, dim = e - j * D;
       const float L = wl[j], O = wo[j * ostride + dim];
@@ -268,7 +298,7 @@ __device__ __forceinline__ void finish_workgroup(const DecodeArgs &a, int b, int
   // partials: (m, l) and o of this split, 16 bytes per access
   for (int u = tid; u < gn * nd4; u += nthr) {
     const int j = u / nd4, d0 = 4 * (u - j * nd4);
-    const uint32_t row = (uint32_t)((bq0 + j) * nsplit + split);
+    const uint32_t row = (uint32_t)((bq0 + j) * nsplit + slot);
     const uint32_t base = row * (uint32_t)D * 4u;
     const float *o = wo + j * ostride + d0;
     if (vec) {
@@ -279,11 +309,6 @@ __device__ __forceinline__ void finish_workgroup(const DecodeArgs &a, int b, int
     if (d0 == 0) store_dev2(rml, row * 8u, f2v_t{wm[j], wl[j]});
   }
 
-  // Splits holding tokens of this sequence (a shorter sequence of a ragged
-  // batch leaves the later splits empty; their workgroups exit at once and
-  // take no ticket).  Split 0 also answers an empty sequence.
-  const int64_t T = seq_len_of(a, b);
-  const int live = (int)max((int64_t)1, min((int64_t)nsplit, (T + a.split_len - 1) / a.split_len));
   __shared__ int s_last;
   __builtin_amdgcn_s_waitcnt(0);  // this thread's partial stores are complete
   __syncthreads();
@@ -371,13 +396,9 @@ inline void carve_workspace(DecodeArgs &a, void *ws) {
 // workgroup capacity.  The plan never has more splits than the one
 // cq_decode_workspace_size sizes for (fewer groups per split there, and the
 // largest capacity of any decode kernel).
-inline int prepare_launch(DecodeArgs &a, int chunk_heads, int64_t resident, void *workspace,
-                          size_t ws_bytes) {
-  a.chunk_heads = chunk_heads;
-  a.n_chunks = (a.G + chunk_heads - 1) / chunk_heads;
-  const SplitPlan p = plan_splits((int64_t)a.B * a.H * a.n_chunks, a.max_T, resident);
-  a.nsplit = p.nsplit;
-  a.split_len = p.split_len;
+// Workspace for a.nsplit partial slots per (sequence, q head) (none needed
+// for one).
+inline int setup_workspace(DecodeArgs &a, void *workspace, size_t ws_bytes) {
   if (a.nsplit > 1) {
     if ((int64_t)a.B * a.H * a.n_chunks > kMaxCounters) return CQ_ERR_UNSUPPORTED;
     // the split partials are addressed with 32-bit byte offsets
@@ -391,6 +412,24 @@ inline int prepare_launch(DecodeArgs &a, int chunk_heads, int64_t resident, void
     a.counters = nullptr;
   }
   return CQ_OK;
+}
+
+// Grid-plan launch preparation: split plan and workspace.
+inline int prepare_launch(DecodeArgs &a, int chunk_heads, int64_t resident, void *workspace,
+                          size_t ws_bytes) {
+  a.chunk_heads = chunk_heads;
+  a.n_chunks = (a.G + chunk_heads - 1) / chunk_heads;
+  const SplitPlan p = plan_splits((int64_t)a.B * a.H * a.n_chunks, a.max_T, resident);
+  a.nsplit = p.nsplit;
+  a.split_len = p.split_len;
+  return setup_workspace(a, workspace, ws_bytes);
+}
+
+// Balanced-plan partial slots per sequence for P workgroups per column: a
+// sequence spans at most min(P, units of the length bound) workgroups.
+inline int64_t balanced_slots(int64_t P, int64_t max_T) {
+  const int64_t n = units_of(max_T);
+  return P < n ? P : n;
 }
 
 int launch_decode_mfma(DecodeArgs &a, void *workspace, size_t ws_bytes, hipStream_t stream);

@@ -80,348 +80,422 @@ struct G4Buf {
 
 }  // namespace
 
+// kBalanced = false: grid plan, workgroup (split, kv head, sequence) takes
+// tokens [split * split_len, +split_len) of one sequence (uniform batches,
+// where it is as balanced as the partition below).  kBalanced = true: the
+// balanced partition of the batch's units (cq_plan.h), one or more segments
+// per workgroup.
+template <bool kBalanced>
 __global__ __launch_bounds__(kThreadsMfma) void decode_g4_kernel(DecodeArgs a) {
   __shared__ G4Lds lds;
+  __shared__ int32_t s_units[kBalanced ? kMaxTableSeqs + 1 : 1];
+  // Balanced plan: workgroup p of the column takes units [floor(pU/P),
+  // floor((p+1)U/P)) of the batch's units laid end to end, one segment per
+  // sequence it touches.  Per-sequence lengths give the unit table;
+  // otherwise every sequence has the units of the length bound.
+  //
+  // The loop state stays in LDS while a segment runs and is read back after
+  // it (the cursor double-buffered by iteration parity: thread 0 writes the
+  // next cursor while other waves may still read the current one), so the
+  // segment body keeps the scalar registers of a one-segment kernel.
+  __shared__ int32_t s_loop[8];  // cursor unit [2], cursor sequence [2], end unit, P, n
   prefetch_args();
-  const int split = blockIdx.x;
   const int h = blockIdx.y;  // kv head: one q-head chunk (G <= 4)
-  const int b = blockIdx.z;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int col = lane & 15, kg = lane >> 4;
-  const int hq = col & 3;   // score layout: head of this lane's column
-  const int jb = col >> 2;  // score layout: token block of this lane's column
-  const int gn = a.G;
-  const int64_t bh = (int64_t)b * a.H + h;
-  const int64_t T = seq_len_of(a, b);
-  const int64_t t0 = (int64_t)split * a.split_len;
-  const int64_t t1 = min(T, t0 + a.split_len);
-  if (split_is_empty(split, t0, T)) return;
-  const int lsk = __builtin_ctz(a.stride[0]), lsv = __builtin_ctz(a.stride[1]);
-  const int mk = a.stride[0] - 1, mv = a.stride[1] - 1;
-
-  const __amdgpu_buffer_rsrc_t r_kfk =
-      make_rsrc(a.kf[0] + bh * a.cap_kf[0] * kD, (uint32_t)(a.cap_kf[0] * kD * 2));
-  const __amdgpu_buffer_rsrc_t r_kfv =
-      make_rsrc(a.kf[1] + bh * a.cap_kf[1] * kD, (uint32_t)(a.cap_kf[1] * kD * 2));
-  const __amdgpu_buffer_rsrc_t r_pkk =
-      make_rsrc(a.pk[0] + bh * a.cap_pf[0] * 16, (uint32_t)(a.cap_pf[0] * 64));
-  const __amdgpu_buffer_rsrc_t r_pkv =
-      make_rsrc(a.pk[1] + bh * a.cap_pf[1] * 16, (uint32_t)(a.cap_pf[1] * 64));
-  const __amdgpu_buffer_rsrc_t r_sck = make_rsrc(a.sc[0] + bh * a.cap_pf[0], (uint32_t)(a.cap_pf[0] * 2));
-  const __amdgpu_buffer_rsrc_t r_scv = make_rsrc(a.sc[1] + bh * a.cap_pf[1], (uint32_t)(a.cap_pf[1] * 2));
-
-  G4GroupScratch &Gs = lds.s.g;
-  G4WaveScratch &W = lds.s.w[wave];
-
-  // Stage the chunk at c0 into cb: the token phase (lane = token c0 + lane:
-  // scales, own K code row, V slot to LDS), then the K anchor rows and the V
-  // code words.  A chunk past the end (nt = 0) gets offsets past every buffer,
-  // so its loads return zeros without traffic; so do I-frame and padding slots.
-  auto stage = [&](int c0, G4Buf &cb) {
-    const int nt = (int)max((int64_t)0, min((int64_t)kChunk, t1 - c0));
-    cb.c0 = c0;
-    cb.nt = nt;
-    const int gk_base = c0 >> lsk;
-    const int gk_last = nt ? (c0 + nt - 1) >> lsk : gk_base;
-    // anchor offsets stay below 2^30; buffers are below 2^31 bytes (mfma_supported)
-    const uint32_t dead = nt ? 0u : 0x80000000u;
-    {
-      const bool valid = lane < nt;
-      const int t = c0 + lane;
-      const int slk = (valid && (t & mk)) ? t - (t >> lsk) - 1 : -1;
-      const int slv = (valid && (t & mv)) ? t - (t >> lsv) - 1 : -1;
-      // slot -1 reads past the buffer: scale 0, codes 0
-      cb.sk = bload16(r_sck, (uint32_t)slk * 2u);
-      cb.sv = bload16(r_scv, (uint32_t)slv * 2u);
-#pragma unroll
-      // the row's 4 quarters: each load touches every 64-byte row of the chunk
-      // once, so these stay cacheable for the next three (no nt policy)
-      for (int q = 0; q < 4; ++q) {
-        const i4_t v = __builtin_amdgcn_raw_buffer_load_b128(r_pkk, (int)((uint32_t)slk * 64u + 16u * q), 0, 0);
-        cb.kr[q] = uint4{(uint32_t)v[0], (uint32_t)v[1], (uint32_t)v[2], (uint32_t)v[3]};
-      }
-      W.slot_v[lane] = slv;
+  const bool table = kBalanced && a.seq_lens && a.B > 1 && a.B <= kMaxTableSeqs;
+  if constexpr (kBalanced) {
+    if (table) build_unit_table(a, s_units);
+    UnitSpace us;
+    us.start = table ? s_units : nullptr;
+    us.n = units_of(a.max_T);
+    us.B = a.B;
+    const int64_t U = us.total();
+    const int64_t P = min((int64_t)gridDim.x, U);  // every workgroup below P has units
+    if ((int64_t)blockIdx.x >= P) return;
+    if (threadIdx.x == 0) {
+      const int64_t u0 = unit_begin(blockIdx.x, U, P);
+      s_loop[0] = (int32_t)u0;
+      s_loop[2] = us.seq_of(u0);
+      s_loop[4] = (int32_t)unit_begin(blockIdx.x + 1, U, P);
+      s_loop[5] = (int32_t)P;
+      s_loop[6] = (int32_t)us.n;
     }
-    wave_lds_sync();
-    {
-      const uint32_t row = ((uint32_t)min(gk_base + col, gk_last) * 256u + 64u * kg) | dead;
-#pragma unroll
-      for (int kb = 0; kb < 4; ++kb) cb.ka[kb] = bload128(r_kfk, row + 16u * kb);
-    }
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int4 sl4 = *(const int4 *)&W.slot_v[16 * i + 4 * kg];
-      cb.vw[i][0] = bload32(r_pkv, (uint32_t)sl4.x * 64u + 4u * col);
-      cb.vw[i][1] = bload32(r_pkv, (uint32_t)sl4.y * 64u + 4u * col);
-      cb.vw[i][2] = bload32(r_pkv, (uint32_t)sl4.z * 64u + 4u * col);
-      cb.vw[i][3] = bload32(r_pkv, (uint32_t)sl4.w * 64u + 4u * col);
-    }
-  };
-  // V anchor rows gv_base + 4kg + r of the chunk at c0, dims 8col .. 8col+7.
-  uint4 va[4];
-  auto stage_va = [&](int c0) {
-    const int nt = (int)max((int64_t)0, min((int64_t)kChunk, t1 - c0));
-    const int gv_base = c0 >> lsv;
-    const int gv_last = nt ? (c0 + nt - 1) >> lsv : gv_base;
-    const uint32_t dead = nt ? 0u : 0x80000000u;
-#pragma unroll
-    for (int r = 0; r < 4; ++r)
-      va[r] = bload128(r_kfv, ((uint32_t)min(gv_base + 4 * kg + r, gv_last) * 256u + 16u * col) | dead);
-  };
-
-  // The first chunk's loads go out before the q table is built, so the two
-  // round trips overlap.
-  int64_t c0l = t0 + (int64_t)wave * kChunk;
-  const bool has_work = c0l < t1;
-  G4Buf bufA, bufB;
-  if (has_work) {
-    stage((int)c0l, bufA);
-    stage_va((int)c0l);
+    __syncthreads();
   }
-
-  // ---- q table: q' = fp16(q * fp16(scale)) (bf16 queries: bf16(q * bf16(scale)))
-  // per (slab m, head), in the order {d0, d4, d1, d5, d2, d6, d3, d7} that
-  // unpack_k gives a code word's nibbles; heads >= gn are zero.
-  if (tid < 64) {
-    const int hh = tid >> 4, m = tid & 15;
-    h8_t v = {};
-    float part = 0.f;
-    if (hh < gn) {
-      const uint4 raw =
-          *(const uint4 *)((const uint16_t *)a.q + ((int64_t)b * a.nq + h * a.G + hh) * kD + 8 * m);
-      const h8_t x = a.q_dtype == CQ_BF16 ? bf16x8_scaled_to_f16(raw, bf16_round(a.scale))
-                                          : __builtin_bit_cast(h8_t, raw) * (_Float16)a.scale;
-      v = h8_t{x[0], x[4], x[1], x[5], x[2], x[6], x[3], x[7]};
-#pragma unroll
-      for (int e = 0; e < 8; ++e) part += (float)x[e];
-    }
-    Gs.q[m][hh] = v;
-    part += __shfl_xor(part, 1, 64);
-    part += __shfl_xor(part, 2, 64);
-    part += __shfl_xor(part, 4, 64);
-    part += __shfl_xor(part, 8, 64);
-    if (m == 0) Gs.s8[hh] = 8.f * part;
-  } else if (tid < 128) {
-    (&Gs.zero[0][0])[tid - 64] = h8_t{};
-  }
-  __syncthreads();
-  // score-layout B operand of slab m: Gs.q[m][hq] on the diagonal blocks, else zeros
-  const h8_t *qsrc = jb == kg ? &Gs.q[0][hq] : &Gs.zero[0][hq];
-  // 16-head-layout B operand of the anchor product (q'^T, column = head)
-  const h8_t *qcol = col < kG4 ? &Gs.q[0][col] : &Gs.zero[0][0];
-  const float s8l = Gs.s8[hq] * kLog2e;
-
-  uint32_t magic;  // fp16 1024 in both halves, held in a VGPR for v_and_or_b32
-  asm volatile("v_mov_b32 %0, 0x64006400" : "=v"(magic));
-
-  // score layout: softmax state of head hq (identical across its 16 lanes)
-  float m_run = -INFINITY;  // log2 units
-  float l_run = 0.f;        // sum of fp16 p over this lane's tokens
-  float w_run = 0.f;        // sum of fp16 p*s_v
-  float x_run = 0.f;        // sum of fp16 p*s_v/16
-  f4_t acc[8];
-#pragma unroll
-  for (int nb = 0; nb < 8; ++nb) acc[nb] = f4_t{0.f, 0.f, 0.f, 0.f};
-  const h2_t ones = {(_Float16)1.f, (_Float16)1.f};
-  const h2_t sixteenth = {(_Float16)0.0625f, (_Float16)0.0625f};
-
-  auto compute = [&](G4Buf &cb, int sl) {
-    const int c0 = cb.c0;
-    const int gk_base = c0 >> lsk, gv_base = c0 >> lsv;
-    W.s16[sl][lane] = cb.sk | (cb.sv << 16);
-    // ---- anchor table: log2e * q'.a - mref for anchors gk_base + 4kg + r ----------
-    // (C[anchor][head col]; the lanes col < 4 are head col's score lanes of
-    // block 0, whose m_run is head col's)
-    {
-      f4_t d = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int kb = 0; kb < 4; ++kb) d = mfma32(korder(cb.ka[kb]), qcol[(4 * kg + kb) * kG4], d);
-      if (col < kG4) {
-        const float mref = (m_run == -INFINITY) ? 0.f : m_run;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) W.qa[4 * kg + r][col] = __builtin_fmaf(d[r], kLog2e, -mref);
+  for (int it = 0;; ++it) {
+    const int tid = thread_id();
+    const int lane = tid & 63, wave = tid >> 6;
+    const int col = lane & 15, kg = lane >> 4;
+    const int hq = col & 3;   // score layout: head of this lane's column
+    const int jb = col >> 2;  // score layout: token block of this lane's column
+    const int gn = a.G;
+    const int lsk = __builtin_ctz(a.stride[0]), lsv = __builtin_ctz(a.stride[1]);
+    const int mk = a.stride[0] - 1, mv = a.stride[1] - 1;
+    int b, slot, live;
+    int64_t t0, t1;
+    if constexpr (kBalanced) {
+      const volatile int32_t *sl = s_loop;
+      const int32_t u = __builtin_amdgcn_readfirstlane(sl[it & 1]);
+      if (u >= __builtin_amdgcn_readfirstlane(sl[4])) break;
+      b = __builtin_amdgcn_readfirstlane(sl[2 + (it & 1)]);
+      UnitSpace us;
+      us.start = table ? s_units : nullptr;
+      us.n = __builtin_amdgcn_readfirstlane(sl[6]);
+      us.B = a.B;
+      Segment sg;
+      const int64_t u_next = segment_at(us, blockIdx.x, __builtin_amdgcn_readfirstlane(sl[5]), u,
+                                        b, seq_len_of(a, b), sg);
+      if (tid == 0) {
+        s_loop[(it + 1) & 1] = (int32_t)u_next;
+        s_loop[2 + ((it + 1) & 1)] = b + 1;
       }
+      if (sg.live == 0) {  // past the sequence's end
+        __syncthreads();
+        continue;
+      }
+      t0 = sg.t0;
+      t1 = sg.t1;
+      slot = sg.slot;
+      live = sg.live;
+    } else {
+      const int split = blockIdx.x;
+      b = blockIdx.z;
+      const int64_t T = seq_len_of(a, b);
+      t0 = (int64_t)split * a.split_len;
+      t1 = min(T, t0 + a.split_len);
+      if (split_is_empty(split, t0, T)) return;
+      slot = split;
+      live = grid_live(a, T);
     }
-    wave_lds_sync();
+    const int64_t bh = (int64_t)b * a.H + h;
 
-    // ---- scores of tokens 16 jb + 4 kg + r, head hq (log2 units, minus mref) -------
-    // two independent accumulation chains; each group of 4 q slabs is read
-    // from LDS together
-    f4_t d0 = {0.f, 0.f, 0.f, 0.f}, d1 = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const h8_t b0 = qsrc[(4 * q + 0) * kG4], b1 = qsrc[(4 * q + 1) * kG4];
-      const h8_t b2 = qsrc[(4 * q + 2) * kG4], b3 = qsrc[(4 * q + 3) * kG4];
-      d0 = mfma32(unpack_k(cb.kr[q].x), b0, d0);
-      d1 = mfma32(unpack_k(cb.kr[q].y), b1, d1);
-      d0 = mfma32(unpack_k(cb.kr[q].z), b2, d0);
-      d1 = mfma32(unpack_k(cb.kr[q].w), b3, d1);
-    }
-    const f4_t d = d0 + d1;
-    const int tb = 16 * jb + 4 * kg;
-    const uint4 s4 = *(const uint4 *)&W.s16[sl][tb];
-    const uint32_t sr[4] = {s4.x, s4.y, s4.z, s4.w};
-    // the 4 tokens share one K anchor (stride >= 4, token groups aligned to 4)
-    const float qa = W.qa[((c0 + tb) >> lsk) - gk_base][hq];
-    float sc[4];
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      // log2e * s * (q'.c) with q'.c = 2^24 d - 8 sum(q')
-      const float qc = __builtin_fmaf(d[r], kTwo24 * kLog2e, -s8l);
-      sc[r] = __builtin_fmaf((float)as_h2(sr[r]).x, qc, qa);
-    }
-    // Tokens past the end exist only in a split's last chunk (a uniform branch).
-    if (cb.nt < kChunk) {
-#pragma unroll
+    const __amdgpu_buffer_rsrc_t r_kfk =
+        make_rsrc(a.kf[0] + bh * a.cap_kf[0] * kD, (uint32_t)(a.cap_kf[0] * kD * 2));
+    const __amdgpu_buffer_rsrc_t r_kfv =
+        make_rsrc(a.kf[1] + bh * a.cap_kf[1] * kD, (uint32_t)(a.cap_kf[1] * kD * 2));
+    const __amdgpu_buffer_rsrc_t r_pkk =
+        make_rsrc(a.pk[0] + bh * a.cap_pf[0] * 16, (uint32_t)(a.cap_pf[0] * 64));
+    const __amdgpu_buffer_rsrc_t r_pkv =
+        make_rsrc(a.pk[1] + bh * a.cap_pf[1] * 16, (uint32_t)(a.cap_pf[1] * 64));
+    const __amdgpu_buffer_rsrc_t r_sck = make_rsrc(a.sc[0] + bh * a.cap_pf[0], (uint32_t)(a.cap_pf[0] * 2));
+    const __amdgpu_buffer_rsrc_t r_scv = make_rsrc(a.sc[1] + bh * a.cap_pf[1], (uint32_t)(a.cap_pf[1] * 2));
+
+    G4GroupScratch &Gs = lds.s.g;
+    G4WaveScratch &W = lds.s.w[wave];
+
+    // Stage the chunk at c0 into cb: the token phase (lane = token c0 + lane:
+    // scales, own K code row, V slot to LDS), then the K anchor rows and the V
+    // code words.  A chunk past the end (nt = 0) gets offsets past every buffer,
+    // so its loads return zeros without traffic; so do I-frame and padding slots.
+    auto stage = [&](int c0, G4Buf &cb) {
+      const int nt = (int)max((int64_t)0, min((int64_t)kChunk, t1 - c0));
+      cb.c0 = c0;
+      cb.nt = nt;
+      const int gk_base = c0 >> lsk;
+      const int gk_last = nt ? (c0 + nt - 1) >> lsk : gk_base;
+      // anchor offsets stay below 2^30; buffers are below 2^31 bytes (mfma_supported)
+      const uint32_t dead = nt ? 0u : 0x80000000u;
+      {
+        const bool valid = lane < nt;
+        const int t = c0 + lane;
+        const int slk = (valid && (t & mk)) ? t - (t >> lsk) - 1 : -1;
+        const int slv = (valid && (t & mv)) ? t - (t >> lsv) - 1 : -1;
+        // slot -1 reads past the buffer: scale 0, codes 0
+        cb.sk = bload16(r_sck, (uint32_t)slk * 2u);
+        cb.sv = bload16(r_scv, (uint32_t)slv * 2u);
+  #pragma unroll
+        // the row's 4 quarters: each load touches every 64-byte row of the chunk
+        // once, so these stay cacheable for the next three (no nt policy)
+        for (int q = 0; q < 4; ++q) {
+          const i4_t v = __builtin_amdgcn_raw_buffer_load_b128(r_pkk, (int)((uint32_t)slk * 64u + 16u * q), 0, 0);
+          cb.kr[q] = uint4{(uint32_t)v[0], (uint32_t)v[1], (uint32_t)v[2], (uint32_t)v[3]};
+        }
+        W.slot_v[lane] = slv;
+      }
+      wave_lds_sync();
+      {
+        const uint32_t row = ((uint32_t)min(gk_base + col, gk_last) * 256u + 64u * kg) | dead;
+  #pragma unroll
+        for (int kb = 0; kb < 4; ++kb) cb.ka[kb] = bload128(r_kfk, row + 16u * kb);
+      }
+  #pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int4 sl4 = *(const int4 *)&W.slot_v[16 * i + 4 * kg];
+        cb.vw[i][0] = bload32(r_pkv, (uint32_t)sl4.x * 64u + 4u * col);
+        cb.vw[i][1] = bload32(r_pkv, (uint32_t)sl4.y * 64u + 4u * col);
+        cb.vw[i][2] = bload32(r_pkv, (uint32_t)sl4.z * 64u + 4u * col);
+        cb.vw[i][3] = bload32(r_pkv, (uint32_t)sl4.w * 64u + 4u * col);
+      }
+    };
+    // V anchor rows gv_base + 4kg + r of the chunk at c0, dims 8col .. 8col+7.
+    uint4 va[4] = {};
+    auto stage_va = [&](int c0) {
+      const int nt = (int)max((int64_t)0, min((int64_t)kChunk, t1 - c0));
+      const int gv_base = c0 >> lsv;
+      const int gv_last = nt ? (c0 + nt - 1) >> lsv : gv_base;
+      const uint32_t dead = nt ? 0u : 0x80000000u;
+  #pragma unroll
       for (int r = 0; r < 4; ++r)
-        if (tb + r >= cb.nt) sc[r] = -INFINITY;
+        va[r] = bload128(r_kfv, ((uint32_t)min(gv_base + 4 * kg + r, gv_last) * 256u + 16u * col) | dead);
+    };
+
+    // The first chunk's loads go out before the q table is built, so the two
+    // round trips overlap.
+    int64_t c0l = t0 + (int64_t)wave * kChunk;
+    const bool has_work = c0l < t1;
+    // (zero-initialised: left undefined on a segment without work, they would
+    // be carried from the previous segment and stay live across the body)
+    G4Buf bufA{}, bufB{};
+    if (has_work) {
+      stage((int)c0l, bufA);
+      stage_va((int)c0l);
     }
 
-    // ---- lazy running max (scores are relative to mref already) ---------------------
-    const float mx = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
-    if (__any(m_run == -INFINITY || mx > kTau)) {
-      // chunk max of head hq: its lanes differ in jb (col bits 2, 3) and kg
-      float cm = mx;
-      cm = fmaxf(cm, __shfl_xor(cm, 4, 64));
-      cm = fmaxf(cm, __shfl_xor(cm, 8, 64));
-      cm = fmaxf(cm, __shfl_xor(cm, 16, 64));
-      cm = fmaxf(cm, __shfl_xor(cm, 32, 64));
-      const float mref = (m_run == -INFINITY) ? 0.f : m_run;
-      const float m_new = fmaxf(m_run, mref + cm);
-      const float f = (m_run == -INFINITY) ? 0.f : fast_exp2(m_run - m_new);
-      l_run *= f;
-      w_run *= f;
-      x_run *= f;
-#pragma unroll
+    // ---- q table: q' = fp16(q * fp16(scale)) (bf16 queries: bf16(q * bf16(scale)))
+    // per (slab m, head), in the order {d0, d4, d1, d5, d2, d6, d3, d7} that
+    // unpack_k gives a code word's nibbles; heads >= gn are zero.
+    if (tid < 64) {
+      const int hh = tid >> 4, m = tid & 15;
+      h8_t v = {};
+      float part = 0.f;
+      if (hh < gn) {
+        const uint4 raw =
+            *(const uint4 *)((const uint16_t *)a.q + ((int64_t)b * a.nq + h * a.G + hh) * kD + 8 * m);
+        const h8_t x = a.q_dtype == CQ_BF16 ? bf16x8_scaled_to_f16(raw, bf16_round(a.scale))
+                                            : __builtin_bit_cast(h8_t, raw) * (_Float16)a.scale;
+        v = h8_t{x[0], x[4], x[1], x[5], x[2], x[6], x[3], x[7]};
+  #pragma unroll
+        for (int e = 0; e < 8; ++e) part += (float)x[e];
+      }
+      Gs.q[m][hh] = v;
+      part += __shfl_xor(part, 1, 64);
+      part += __shfl_xor(part, 2, 64);
+      part += __shfl_xor(part, 4, 64);
+      part += __shfl_xor(part, 8, 64);
+      if (m == 0) Gs.s8[hh] = 8.f * part;
+    } else if (tid < 128) {
+      (&Gs.zero[0][0])[tid - 64] = h8_t{};
+    }
+    __syncthreads();
+    // score-layout B operand of slab m: Gs.q[m][hq] on the diagonal blocks, else zeros
+    const h8_t *qsrc = jb == kg ? &Gs.q[0][hq] : &Gs.zero[0][hq];
+    // 16-head-layout B operand of the anchor product (q'^T, column = head)
+    const h8_t *qcol = col < kG4 ? &Gs.q[0][col] : &Gs.zero[0][0];
+    const float s8l = Gs.s8[hq] * kLog2e;
+
+    uint32_t magic;  // fp16 1024 in both halves, held in a VGPR for v_and_or_b32
+    asm volatile("v_mov_b32 %0, 0x64006400" : "=v"(magic));
+
+    // score layout: softmax state of head hq (identical across its 16 lanes)
+    float m_run = -INFINITY;  // log2 units
+    float l_run = 0.f;        // sum of fp16 p over this lane's tokens
+    float w_run = 0.f;        // sum of fp16 p*s_v
+    float x_run = 0.f;        // sum of fp16 p*s_v/16
+    f4_t acc[8];
+  #pragma unroll
+    for (int nb = 0; nb < 8; ++nb) acc[nb] = f4_t{0.f, 0.f, 0.f, 0.f};
+    const h2_t ones = {(_Float16)1.f, (_Float16)1.f};
+    const h2_t sixteenth = {(_Float16)0.0625f, (_Float16)0.0625f};
+
+    auto compute = [&](G4Buf &cb, int sl) {
+      const int c0 = cb.c0;
+      const int gk_base = c0 >> lsk, gv_base = c0 >> lsv;
+      W.s16[sl][lane] = cb.sk | (cb.sv << 16);
+      // ---- anchor table: log2e * q'.a - mref for anchors gk_base + 4kg + r ----------
+      // (C[anchor][head col]; the lanes col < 4 are head col's score lanes of
+      // block 0, whose m_run is head col's)
+      {
+        f4_t d = {0.f, 0.f, 0.f, 0.f};
+  #pragma unroll
+        for (int kb = 0; kb < 4; ++kb) d = mfma32(korder(cb.ka[kb]), qcol[(4 * kg + kb) * kG4], d);
+        if (col < kG4) {
+          const float mref = (m_run == -INFINITY) ? 0.f : m_run;
+  #pragma unroll
+          for (int r = 0; r < 4; ++r) W.qa[4 * kg + r][col] = __builtin_fmaf(d[r], kLog2e, -mref);
+        }
+      }
+      wave_lds_sync();
+
+      // ---- scores of tokens 16 jb + 4 kg + r, head hq (log2 units, minus mref) -------
+      // two independent accumulation chains; each group of 4 q slabs is read
+      // from LDS together
+      f4_t d0 = {0.f, 0.f, 0.f, 0.f}, d1 = {0.f, 0.f, 0.f, 0.f};
+  #pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const h8_t b0 = qsrc[(4 * q + 0) * kG4], b1 = qsrc[(4 * q + 1) * kG4];
+        const h8_t b2 = qsrc[(4 * q + 2) * kG4], b3 = qsrc[(4 * q + 3) * kG4];
+        d0 = mfma32(unpack_k(cb.kr[q].x), b0, d0);
+        d1 = mfma32(unpack_k(cb.kr[q].y), b1, d1);
+        d0 = mfma32(unpack_k(cb.kr[q].z), b2, d0);
+        d1 = mfma32(unpack_k(cb.kr[q].w), b3, d1);
+      }
+      const f4_t d = d0 + d1;
+      const int tb = 16 * jb + 4 * kg;
+      const uint4 s4 = *(const uint4 *)&W.s16[sl][tb];
+      const uint32_t sr[4] = {s4.x, s4.y, s4.z, s4.w};
+      // the 4 tokens share one K anchor (stride >= 4, token groups aligned to 4)
+      const float qa = W.qa[((c0 + tb) >> lsk) - gk_base][hq];
+      float sc[4];
+  #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        // acc row 4kg + r holds head r (rows >= 4 repeat heads r, unused)
-        const float fr = __shfl(f, r, 64);
-#pragma unroll
-        for (int nb = 0; nb < 8; ++nb) acc[nb][r] *= fr;
+        // log2e * s * (q'.c) with q'.c = 2^24 d - 8 sum(q')
+        const float qc = __builtin_fmaf(d[r], kTwo24 * kLog2e, -s8l);
+        sc[r] = __builtin_fmaf((float)as_h2(sr[r]).x, qc, qa);
       }
-      const float shift = ((m_new == -INFINITY) ? 0.f : m_new) - mref;
-#pragma unroll
-      for (int r = 0; r < 4; ++r) sc[r] -= shift;
-      m_run = m_new;
-    }
+      // Tokens past the end exist only in a split's last chunk (a uniform branch).
+      if (cb.nt < kChunk) {
+  #pragma unroll
+        for (int r = 0; r < 4; ++r)
+          if (tb + r >= cb.nt) sc[r] = -INFINITY;
+      }
 
-    // ---- weights: p (fp16), p*s_v and p*s_v/16 (fp16 products) -------------------------
-    {
-      const h2_t p01 = h2_t{(_Float16)fast_exp2(sc[0]), (_Float16)fast_exp2(sc[1])};
-      const h2_t p23 = h2_t{(_Float16)fast_exp2(sc[2]), (_Float16)fast_exp2(sc[3])};
-      const h2_t sv01 = as_h2(__builtin_amdgcn_perm(s4.y, s4.x, 0x07060302u));
-      const h2_t sv23 = as_h2(__builtin_amdgcn_perm(s4.w, s4.z, 0x07060302u));
-      const h2_t w01 = p01 * sv01, w23 = p23 * sv23;
-      const h2_t x01 = w01 * sixteenth, x23 = w23 * sixteenth;
-      l_run = __builtin_amdgcn_fdot2(p01, ones, l_run, false);
-      l_run = __builtin_amdgcn_fdot2(p23, ones, l_run, false);
-      w_run = __builtin_amdgcn_fdot2(w01, ones, w_run, false);
-      w_run = __builtin_amdgcn_fdot2(w23, ones, w_run, false);
-      x_run = __builtin_amdgcn_fdot2(x01, ones, x_run, false);
-      x_run = __builtin_amdgcn_fdot2(x23, ones, x_run, false);
-      // to the V-product operand layout: (head hq, 4-token group 4 jb + kg)
-      const int g4 = 4 * jb + kg;
-      W.pw[0][hq][g4] = uint2{__builtin_bit_cast(uint32_t, p01), __builtin_bit_cast(uint32_t, p23)};
-      W.pw[1][hq][g4] = uint2{__builtin_bit_cast(uint32_t, w01), __builtin_bit_cast(uint32_t, w23)};
-      W.pw[2][hq][g4] = uint2{__builtin_bit_cast(uint32_t, x01), __builtin_bit_cast(uint32_t, x23)};
-    }
-    wave_lds_sync();
+      // ---- lazy running max (scores are relative to mref already) ---------------------
+      const float mx = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
+      if (__any(m_run == -INFINITY || mx > kTau)) {
+        // chunk max of head hq: its lanes differ in jb (col bits 2, 3) and kg
+        float cm = mx;
+        cm = fmaxf(cm, __shfl_xor(cm, 4, 64));
+        cm = fmaxf(cm, __shfl_xor(cm, 8, 64));
+        cm = fmaxf(cm, __shfl_xor(cm, 16, 64));
+        cm = fmaxf(cm, __shfl_xor(cm, 32, 64));
+        const float mref = (m_run == -INFINITY) ? 0.f : m_run;
+        const float m_new = fmaxf(m_run, mref + cm);
+        const float f = (m_run == -INFINITY) ? 0.f : fast_exp2(m_run - m_new);
+        l_run *= f;
+        w_run *= f;
+        x_run *= f;
+  #pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          // acc row 4kg + r holds head r (rows >= 4 repeat heads r, unused)
+          const float fr = __shfl(f, r, 64);
+  #pragma unroll
+          for (int nb = 0; nb < 8; ++nb) acc[nb][r] *= fr;
+        }
+        const float shift = ((m_new == -INFINITY) ? 0.f : m_new) - mref;
+  #pragma unroll
+        for (int r = 0; r < 4; ++r) sc[r] -= shift;
+        m_run = m_new;
+      }
 
-    // ---- P_g and code P.V, two 16-token tiles per K=32 product --------------------------
-    // K index 8kg + e of the products below is token 16(2P) + 4kg + e (e < 4)
-    // or 16(2P+1) + 4kg + e - 4 (e >= 4).  Operand rows are heads (col & 3:
-    // rows >= 4 repeat heads 0..3 and are never read).
-    const int hr = col & 3;
-    f4_t pg = {0.f, 0.f, 0.f, 0.f};  // P_g^T: lane holds groups 4kg+r, head col
-#pragma unroll
-    for (int P = 0; P < 2; ++P) {
-      const uint2 pa = W.pw[0][hr][8 * P + kg], pb = W.pw[0][hr][8 * P + 4 + kg];
-      const uint2 wa = W.pw[1][hr][8 * P + kg], wb = W.pw[1][hr][8 * P + 4 + kg];
-      const uint2 xa = W.pw[2][hr][8 * P + kg], xb = W.pw[2][hr][8 * P + 4 + kg];
-      const h8_t ap = h8_of(pa.x, pa.y, pb.x, pb.y);
-      const h8_t aw = h8_of(wa.x, wa.y, wb.x, wb.y);
-      const h8_t ax = h8_of(xa.x, xa.y, xb.x, xb.y);
-      // E^T: group col x these tokens (fp16 1.0 = 0x3c00); each run of 4
-      // tokens lies in one V group (stride >= 4)
-      const int ga = ((c0 + 32 * P + 4 * kg) >> lsv) - gv_base;
-      const int gb = ((c0 + 32 * P + 16 + 4 * kg) >> lsv) - gv_base;
-      const uint32_t ea = ga == col ? 0x3c003c00u : 0u, eb = gb == col ? 0x3c003c00u : 0u;
-      pg = mfma32(h8_of(ea, ea, eb, eb), ap, pg);
-      // V codes: B = 8 tokens x dim 8col + nb (nibble nb of word col)
-      const int i0 = 2 * P, i1 = 2 * P + 1;
-#pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        const uint32_t sel = (uint32_t)k | (0x0cu << 8) | ((uint32_t)(4 + k) << 16) | (0x0cu << 24);
-        const uint32_t a01 = __builtin_amdgcn_perm(cb.vw[i0][1], cb.vw[i0][0], sel);
-        const uint32_t a23 = __builtin_amdgcn_perm(cb.vw[i0][3], cb.vw[i0][2], sel);
-        const uint32_t b01 = __builtin_amdgcn_perm(cb.vw[i1][1], cb.vw[i1][0], sel);
-        const uint32_t b23 = __builtin_amdgcn_perm(cb.vw[i1][3], cb.vw[i1][2], sel);
-        const h8_t blo = h8_of(and_or(a01, 0x000F000Fu, magic), and_or(a23, 0x000F000Fu, magic),
-                               and_or(b01, 0x000F000Fu, magic), and_or(b23, 0x000F000Fu, magic));
-        const h8_t bhi = h8_of(and_or(a01, 0x00F000F0u, magic), and_or(a23, 0x00F000F0u, magic),
-                               and_or(b01, 0x00F000F0u, magic), and_or(b23, 0x00F000F0u, magic));
-        acc[2 * k] = mfma32(aw, blo, acc[2 * k]);
-        acc[2 * k + 1] = mfma32(ax, bhi, acc[2 * k + 1]);
+      // ---- weights: p (fp16), p*s_v and p*s_v/16 (fp16 products) -------------------------
+      {
+        const h2_t p01 = h2_t{(_Float16)fast_exp2(sc[0]), (_Float16)fast_exp2(sc[1])};
+        const h2_t p23 = h2_t{(_Float16)fast_exp2(sc[2]), (_Float16)fast_exp2(sc[3])};
+        const h2_t sv01 = as_h2(__builtin_amdgcn_perm(s4.y, s4.x, 0x07060302u));
+        const h2_t sv23 = as_h2(__builtin_amdgcn_perm(s4.w, s4.z, 0x07060302u));
+        const h2_t w01 = p01 * sv01, w23 = p23 * sv23;
+        const h2_t x01 = w01 * sixteenth, x23 = w23 * sixteenth;
+        l_run = __builtin_amdgcn_fdot2(p01, ones, l_run, false);
+        l_run = __builtin_amdgcn_fdot2(p23, ones, l_run, false);
+        w_run = __builtin_amdgcn_fdot2(w01, ones, w_run, false);
+        w_run = __builtin_amdgcn_fdot2(w23, ones, w_run, false);
+        x_run = __builtin_amdgcn_fdot2(x01, ones, x_run, false);
+        x_run = __builtin_amdgcn_fdot2(x23, ones, x_run, false);
+        // to the V-product operand layout: (head hq, 4-token group 4 jb + kg)
+        const int g4 = 4 * jb + kg;
+        W.pw[0][hq][g4] = uint2{__builtin_bit_cast(uint32_t, p01), __builtin_bit_cast(uint32_t, p23)};
+        W.pw[1][hq][g4] = uint2{__builtin_bit_cast(uint32_t, w01), __builtin_bit_cast(uint32_t, w23)};
+        W.pw[2][hq][g4] = uint2{__builtin_bit_cast(uint32_t, x01), __builtin_bit_cast(uint32_t, x23)};
+      }
+      wave_lds_sync();
+
+      // ---- P_g and code P.V, two 16-token tiles per K=32 product --------------------------
+      // K index 8kg + e of the products below is token 16(2P) + 4kg + e (e < 4)
+      // or 16(2P+1) + 4kg + e - 4 (e >= 4).  Operand rows are heads (col & 3:
+      // rows >= 4 repeat heads 0..3 and are never read).
+      const int hr = col & 3;
+      f4_t pg = {0.f, 0.f, 0.f, 0.f};  // P_g^T: lane holds groups 4kg+r, head col
+  #pragma unroll
+      for (int P = 0; P < 2; ++P) {
+        const uint2 pa = W.pw[0][hr][8 * P + kg], pb = W.pw[0][hr][8 * P + 4 + kg];
+        const uint2 wa = W.pw[1][hr][8 * P + kg], wb = W.pw[1][hr][8 * P + 4 + kg];
+        const uint2 xa = W.pw[2][hr][8 * P + kg], xb = W.pw[2][hr][8 * P + 4 + kg];
+        const h8_t ap = h8_of(pa.x, pa.y, pb.x, pb.y);
+        const h8_t aw = h8_of(wa.x, wa.y, wb.x, wb.y);
+        const h8_t ax = h8_of(xa.x, xa.y, xb.x, xb.y);
+        // E^T: group col x these tokens (fp16 1.0 = 0x3c00); each run of 4
+        // tokens lies in one V group (stride >= 4)
+        const int ga = ((c0 + 32 * P + 4 * kg) >> lsv) - gv_base;
+        const int gb = ((c0 + 32 * P + 16 + 4 * kg) >> lsv) - gv_base;
+        const uint32_t ea = ga == col ? 0x3c003c00u : 0u, eb = gb == col ? 0x3c003c00u : 0u;
+        pg = mfma32(h8_of(ea, ea, eb, eb), ap, pg);
+        // V codes: B = 8 tokens x dim 8col + nb (nibble nb of word col)
+        const int i0 = 2 * P, i1 = 2 * P + 1;
+  #pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          const uint32_t sel = (uint32_t)k | (0x0cu << 8) | ((uint32_t)(4 + k) << 16) | (0x0cu << 24);
+          const uint32_t a01 = __builtin_amdgcn_perm(cb.vw[i0][1], cb.vw[i0][0], sel);
+          const uint32_t a23 = __builtin_amdgcn_perm(cb.vw[i0][3], cb.vw[i0][2], sel);
+          const uint32_t b01 = __builtin_amdgcn_perm(cb.vw[i1][1], cb.vw[i1][0], sel);
+          const uint32_t b23 = __builtin_amdgcn_perm(cb.vw[i1][3], cb.vw[i1][2], sel);
+          const h8_t blo = h8_of(and_or(a01, 0x000F000Fu, magic), and_or(a23, 0x000F000Fu, magic),
+                                 and_or(b01, 0x000F000Fu, magic), and_or(b23, 0x000F000Fu, magic));
+          const h8_t bhi = h8_of(and_or(a01, 0x00F000F0u, magic), and_or(a23, 0x00F000F0u, magic),
+                                 and_or(b01, 0x00F000F0u, magic), and_or(b23, 0x00F000F0u, magic));
+          acc[2 * k] = mfma32(aw, blo, acc[2 * k]);
+          acc[2 * k + 1] = mfma32(ax, bhi, acc[2 * k + 1]);
+        }
+      }
+
+      // ---- anchor term: P_g as an fp16 hi/lo pair in one K=32 product -------------------
+      // K index 8kg + e: group 4kg + e, hi part (e < 4) or lo part (e >= 4); the
+      // anchor rows are duplicated in the B operand to match.
+      {
+        const h2_t ph01 = h2_t{(_Float16)pg[0], (_Float16)pg[1]};
+        const h2_t ph23 = h2_t{(_Float16)pg[2], (_Float16)pg[3]};
+        const h2_t pl01 = h2_t{(_Float16)(pg[0] - (float)ph01.x), (_Float16)(pg[1] - (float)ph01.y)};
+        const h2_t pl23 = h2_t{(_Float16)(pg[2] - (float)ph23.x), (_Float16)(pg[3] - (float)ph23.y)};
+        const h8_t pa = h8_t{ph01.x, ph01.y, ph23.x, ph23.y, pl01.x, pl01.y, pl23.x, pl23.y};
+  #pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          const h4_t blo = rows_operand(va, k, false), bhi = rows_operand(va, k, true);
+          acc[2 * k] = mfma32(pa, h8_t{blo[0], blo[1], blo[2], blo[3], blo[0], blo[1], blo[2], blo[3]},
+                              acc[2 * k]);
+          acc[2 * k + 1] = mfma32(pa, h8_t{bhi[0], bhi[1], bhi[2], bhi[3], bhi[0], bhi[1], bhi[2], bhi[3]},
+                                  acc[2 * k + 1]);
+        }
+      }
+    };
+
+    // Software pipeline: the next chunk's loads are issued before the current
+    // chunk is computed (two register buffers, unrolled by two).
+    if (has_work) {
+      for (;;) {
+        stage((int)(c0l + kWaves * kChunk), bufB);
+        compute(bufA, 0);
+        c0l += kWaves * kChunk;
+        if (c0l >= t1) break;
+        stage_va((int)c0l);
+        stage((int)(c0l + kWaves * kChunk), bufA);
+        compute(bufB, 1);
+        c0l += kWaves * kChunk;
+        if (c0l >= t1) break;
+        stage_va((int)c0l);
       }
     }
 
-    // ---- anchor term: P_g as an fp16 hi/lo pair in one K=32 product -------------------
-    // K index 8kg + e: group 4kg + e, hi part (e < 4) or lo part (e >= 4); the
-    // anchor rows are duplicated in the B operand to match.
-    {
-      const h2_t ph01 = h2_t{(_Float16)pg[0], (_Float16)pg[1]};
-      const h2_t ph23 = h2_t{(_Float16)pg[2], (_Float16)pg[3]};
-      const h2_t pl01 = h2_t{(_Float16)(pg[0] - (float)ph01.x), (_Float16)(pg[1] - (float)ph01.y)};
-      const h2_t pl23 = h2_t{(_Float16)(pg[2] - (float)ph23.x), (_Float16)(pg[3] - (float)ph23.y)};
-      const h8_t pa = h8_t{ph01.x, ph01.y, ph23.x, ph23.y, pl01.x, pl01.y, pl23.x, pl23.y};
-#pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        const h4_t blo = rows_operand(va, k, false), bhi = rows_operand(va, k, true);
-        acc[2 * k] = mfma32(pa, h8_t{blo[0], blo[1], blo[2], blo[3], blo[0], blo[1], blo[2], blo[3]},
-                            acc[2 * k]);
-        acc[2 * k + 1] = mfma32(pa, h8_t{bhi[0], bhi[1], bhi[2], bhi[3], bhi[0], bhi[1], bhi[2], bhi[3]},
-                                acc[2 * k + 1]);
-      }
+    // ---- totals of head hq: its 16 lanes hold disjoint tokens ---------------------------
+  #pragma unroll
+    for (int x = 4; x < 64; x *= 2) {
+      l_run += __shfl_xor(l_run, x, 64);
+      w_run += __shfl_xor(w_run, x, 64);
+      x_run += __shfl_xor(x_run, x, 64);
     }
-  };
-
-  // Software pipeline: the next chunk's loads are issued before the current
-  // chunk is computed (two register buffers, unrolled by two).
-  if (has_work) {
-    for (;;) {
-      stage((int)(c0l + kWaves * kChunk), bufB);
-      compute(bufA, 0);
-      c0l += kWaves * kChunk;
-      if (c0l >= t1) break;
-      stage_va((int)c0l);
-      stage((int)(c0l + kWaves * kChunk), bufA);
-      compute(bufB, 1);
-      c0l += kWaves * kChunk;
-      if (c0l >= t1) break;
-      stage_va((int)c0l);
+    float sw[4], sx[4];
+  #pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      sw[r] = __shfl(w_run, r, 64);  // lane r: head r
+      sx[r] = __shfl(x_run, r, 64);
     }
+    // merge_and_finish reads (m, l) of head col from the lanes col < 4 of kg 0:
+    // head col's score lanes of block 0.  Code columns: x = 1032 + c (even nb,
+    // weight p s) or 1152 + 16c (odd nb, weight p s / 16).
+    merge_and_finish(a, lds.mg, b, h, 0, 0, gn, slot, live, m_run, l_run, [&](int nb, int r) {
+      const float corr = (nb & 1) ? 1024.f * sx[r] + 8.f * sw[r] : 1032.f * sw[r];
+      return acc[nb][r] - corr;
+    });
+    if constexpr (!kBalanced) return;
+    __syncthreads();  // the next segment's staging reuses the merge area
   }
-
-  // ---- totals of head hq: its 16 lanes hold disjoint tokens ---------------------------
-#pragma unroll
-  for (int x = 4; x < 64; x *= 2) {
-    l_run += __shfl_xor(l_run, x, 64);
-    w_run += __shfl_xor(w_run, x, 64);
-    x_run += __shfl_xor(x_run, x, 64);
-  }
-  float sw[4], sx[4];
-#pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    sw[r] = __shfl(w_run, r, 64);  // lane r: head r
-    sx[r] = __shfl(x_run, r, 64);
-  }
-  // merge_and_finish reads (m, l) of head col from the lanes col < 4 of kg 0:
-  // head col's score lanes of block 0.  Code columns: x = 1032 + c (even nb,
-  // weight p s) or 1152 + 16c (odd nb, weight p s / 16).
-  merge_and_finish(a, lds.mg, b, h, 0, 0, gn, split, m_run, l_run, [&](int nb, int r) {
-    const float corr = (nb & 1) ? 1024.f * sx[r] + 8.f * sw[r] : 1032.f * sw[r];
-    return acc[nb][r] - corr;
-  });
 }
 
 // ---------------------------------------------------------------------------
@@ -433,15 +507,50 @@ bool g4_supported(const DecodeArgs &a) {
 }
 
 int64_t g4_resident() {
-  return resident_workgroups(reinterpret_cast<const void *>(decode_g4_kernel), kThreadsMfma,
+  return resident_workgroups(reinterpret_cast<const void *>(decode_g4_kernel<true>), kThreadsMfma,
                              kSlotG4);
 }
 
+// Uniform batches (one length bound, or one sequence) take the grid plan
+// unless the balanced partition gives its busiest workgroup fewer units;
+// per-sequence lengths always take the balanced partition.  Both plan one
+// resident generation of workgroups.  Balanced: P workgroups per kv head
+// (never more than the batch has units), and a sequence spans at most
+// balanced_slots(P, max_T) of them, the partial slots per sequence.
 int launch_decode_g4(DecodeArgs &a, void *workspace, size_t ws_bytes, hipStream_t stream) {
-  int st = prepare_launch(a, kG4, g4_resident(), workspace, ws_bytes);
+  a.chunk_heads = kG4;
+  a.n_chunks = 1;
+  const int64_t resident = g4_resident();
+  const int64_t n_max = units_of(a.max_T);
+  int64_t P = std::max((int64_t)1, resident / a.H);
+  P = std::min(P, (int64_t)a.B * n_max);
+  bool balanced = a.seq_lens && a.B > 1;
+  if (!balanced) {
+    const SplitPlan g = plan_splits((int64_t)a.B * a.H, a.max_T, resident);
+    const int64_t grid_units = g.split_len / kUnit;
+    const int64_t bal_units = ((int64_t)a.B * n_max + P - 1) / P;
+    if (bal_units < grid_units) {
+      balanced = true;
+    } else {
+      a.nsplit = g.nsplit;
+      a.split_len = g.split_len;
+    }
+  }
+  if (balanced) {
+    // unit indices are 32-bit in the kernel
+    if ((int64_t)a.B * n_max >= ((int64_t)1 << 31)) return CQ_ERR_UNSUPPORTED;
+    a.nsplit = (int)balanced_slots(P, a.max_T);
+    a.split_len = kUnit;
+  }
+  int st = setup_workspace(a, workspace, ws_bytes);
   if (st) return st;
-  const dim3 grid((unsigned)a.nsplit, (unsigned)a.H, (unsigned)a.B);
-  decode_g4_kernel<<<grid, dim3(kThreadsMfma), 0, stream>>>(a);
+  if (balanced) {
+    const dim3 grid((unsigned)P, (unsigned)a.H, 1u);
+    decode_g4_kernel<true><<<grid, dim3(kThreadsMfma), 0, stream>>>(a);
+  } else {
+    const dim3 grid((unsigned)a.nsplit, (unsigned)a.H, (unsigned)a.B);
+    decode_g4_kernel<false><<<grid, dim3(kThreadsMfma), 0, stream>>>(a);
+  }
   return hipGetLastError() == hipSuccess ? CQ_OK : CQ_ERR_LAUNCH;
 }
 

@@ -138,6 +138,15 @@ __device__ __forceinline__ uint32_t group_or(uint32_t v) {
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// threadIdx.x as a value the optimiser cannot hoist: inside a loop of a long
+// kernel body, addresses derived from the thread index would otherwise be
+// computed once before the loop and all stay live across the body.
+__device__ __forceinline__ int thread_id() {
+  int t = threadIdx.x;
+  asm volatile("" : "+v"(t));
+  return t;
+}
+
 constexpr float kLog2e = 1.4426950408889634f;
 
 }  // namespace cq

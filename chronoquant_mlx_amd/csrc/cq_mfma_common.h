@@ -150,9 +150,9 @@ struct MergeScratch {
 // running maxima itself.  Up to kMergeHeads heads per pass.
 template <typename OVal>
 __device__ __forceinline__ void merge_and_finish(const DecodeArgs &a, MergeScratch &M, int b,
-                                                 int h, int chunk, int j0, int gn, int split,
-                                                 float m_run, float l_run, OVal o_val) {
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+                                                 int h, int chunk, int j0, int gn, int slot,
+                                                 int live, float m_run, float l_run, OVal o_val) {
+  const int tid = thread_id(), lane = tid & 63, wave = tid >> 6;
   const int col = lane & 15, kg = lane >> 4;
   __syncthreads();  // wave scratch becomes the merge area
   if (kg == 0) {
@@ -200,7 +200,7 @@ __device__ __forceinline__ void merge_and_finish(const DecodeArgs &a, MergeScrat
     }
     __syncthreads();
   }
-  finish_workgroup(a, b, h, chunk, j0, gn, split, M.wm, M.wl, &M.o[0][0], kD);
+  finish_workgroup(a, b, h, chunk, j0, gn, slot, live, M.wm, M.wl, &M.o[0][0], kD);
 }
 
 }  // namespace cq

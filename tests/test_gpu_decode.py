@@ -157,6 +157,53 @@ def test_ragged_lengths(generic, lens):
                          mfma=not generic)
 
 
+@pytest.mark.parametrize("B,H,T,seed", [(40, 8, 3000, 41), (1030, 1, 96, 42)])
+def test_balanced_plan_many_sequences(B, H, T, seed):
+    # The GQA-4 kernel lays the batch's 512-token units end to end and gives
+    # every workgroup of a kv head the same share, so a workgroup's range
+    # ends one sequence and starts the next, and a sequence's pieces combine
+    # across workgroups.  B=40 uses the per-sequence unit table (lengths
+    # 0..3000); B=1030 is past the table's 1024 sequences and takes the
+    # uniform unit space, where each workgroup covers several sequences.
+    rng = np.random.default_rng(seed)
+    D, G = 128, 4
+    k = np.cumsum(rng.standard_normal((B, H, T, D)) * 0.1, axis=2).astype(np.float16)
+    v = np.cumsum(rng.standard_normal((B, H, T, D)) * 0.1, axis=2).astype(np.float16)
+    q = rng.standard_normal((B, G * H, D)).astype(np.float16)
+    lens = rng.integers(0, T + 1, size=B)
+    lens[:3] = [0, T, 1]
+    params = dict(stride_k=32, stride_v=8)
+    cache = build_gpu_cache(k, v, **params)
+    scale = D ** -0.5
+    for _ in range(2):
+        out = decode_gpu(cache, q, scale, seq_lens=lens.tolist())
+        for b, L in enumerate(lens.tolist()):
+            if L == 0:
+                assert np.array_equal(out[b], np.zeros_like(out[b])), f"b={b} L=0"
+                continue
+            ck, cv = build_oracle(k[b, :, :L], v[b, :, :L], **params)
+            assert_tight(out[b], O.sdpa_fused(q[b], ck, cv, scale), what=f"b={b} L={L}")
+            if b < 8:
+                assert_close(out[b], oracle_fallback(ck, cv, q[b], scale), what=f"b={b} L={L}")
+
+
+def test_uniform_batch_ranges_across_sequences():
+    # 3 sequences of 16384 tokens over 32 workgroups per kv head: 3 units per
+    # workgroup, so some workgroups end one sequence and start the next.
+    rng = np.random.default_rng(43)
+    B, H, T, D, G = 3, 8, 16384, 128, 4
+    k = np.cumsum(rng.standard_normal((B, H, T, D)) * 0.05, axis=2).astype(np.float16)
+    v = np.cumsum(rng.standard_normal((B, H, T, D)) * 0.05, axis=2).astype(np.float16)
+    q = rng.standard_normal((B, G * H, D)).astype(np.float16)
+    params = dict(stride_k=32, stride_v=8)
+    cache = build_gpu_cache(k, v, **params)
+    scale = D ** -0.5
+    out = decode_gpu(cache, q, scale)
+    for b in range(B):
+        ck, cv = build_oracle(k[b], v[b], **params)
+        assert_tight(out[b], O.sdpa_fused(q[b], ck, cv, scale), what=f"b={b}")
+
+
 def test_output_dtypes_and_fp32_queries():
     from chronoquant_mlx_amd.kernels import chronoquant_sdpa_kernel
     rng = np.random.default_rng(5)
