@@ -200,7 +200,7 @@ __global__ __launch_bounds__(256) void decode_generic_kernel(DecodeArgs a) {
     s_acc[0][j][dim] = O;  // each (j, dim) is read and rewritten by one thread
   }
   __syncthreads();
-  finish_workgroup(a, b, h, chunk, j0, gn, split, grid_live(a, T), w_m, w_l, &s_acc[0][0][0],
+  finish_workgroup(a, b, h, chunk, j0, gn, split, kGridLive, w_m, w_l, &s_acc[0][0][0],
                    kMaxHeadDim);
 }
 

@@ -81,6 +81,7 @@ __device__ __forceinline__ bool split_is_empty(int split, int64_t t0, int64_t T)
 __device__ __forceinline__ int grid_live(const DecodeArgs &a, int64_t T) {
   return (int)max((int64_t)1, min((int64_t)a.nsplit, (T + a.split_len - 1) / a.split_len));
 }
+constexpr int kGridLive = -1;  // finish_workgroup: live count from the grid plan
 
 // Balanced plan (cq_plan.h): start[b] = first unit of sequence b, start[B] =
 // total units, for per-sequence lengths.  Wave 0 scans 64 sequences at a
@@ -173,7 +174,7 @@ template <bool Vec>
 __device__ __forceinline__ void merge_partials(const DecodeArgs &a, __amdgpu_buffer_rsrc_t racc,
                                                __amdgpu_buffer_rsrc_t rml, int64_t bq0, int gn,
                                                int nsplit) {
-  const int tid = thread_id(), nthr = blockDim.x;
+  const int tid = threadIdx.x, nthr = blockDim.x;
   const int D = a.D, nd4 = (D + 3) / 4;
   const int units = gn * nd4;
   int slices = 1;
@@ -261,10 +262,11 @@ __device__ __forceinline__ void merge_partials(const DecodeArgs &a, __amdgpu_buf
 // Per-workgroup epilogue.  The workgroup's merged state for q heads
 // j0 .. j0+gn-1 of kv head h is in LDS: wm[j] (running max, log2 units),
 // wl[j] (sum of weights), wo[j*ostride + d] (unnormalised output).  `live`
-// workgroups share sequence b; this one holds partial slot `slot`.  With
-// live == 1 it writes the output; otherwise it writes its partial, and the
-// last of the live workgroups of (b, h, chunk) to finish merges all partials
-// and resets the counter it used.
+// workgroups share sequence b (kGridLive: the grid plan's splits holding
+// tokens, derived here while the partial stores are in flight); this one
+// holds partial slot `slot`.  With one live workgroup it writes the output;
+// otherwise it writes its partial, and the last of the live workgroups of
+// (b, h, chunk) to finish merges all partials and resets the counter it used.
 //
 // The merge costs one memory round trip: a thread owns (head, 4 dims) and a
 // slice of the splits, issues every load of its splits ((m, l) pairs and
@@ -276,11 +278,11 @@ __device__ __forceinline__ void finish_workgroup(const DecodeArgs &a, int b, int
                                                  int j0, int gn, int slot, int live,
                                                  const float *wm, const float *wl,
                                                  const float *wo, int ostride) {
-  const int tid = thread_id(), nthr = blockDim.x;
+  const int tid = threadIdx.x, nthr = blockDim.x;
   const int D = a.D, nd4 = (D + 3) / 4;
   const bool vec = (D & 3) == 0;  // 16-byte partial accesses
   const int64_t bq0 = (int64_t)b * a.nq + h * a.G + j0;
-  if (live == 1) {
+  if (live == kGridLive ? a.nsplit == 1 : live == 1) {
     for (int e = tid; e < gn * D; e += nthr) {
       const int j = e / D, dim = e - j * D;
       const float L = wl[j], O = wo[j * ostride + dim];
@@ -309,6 +311,7 @@ __device__ __forceinline__ void finish_workgroup(const DecodeArgs &a, int b, int
     if (d0 == 0) store_dev2(rml, row * 8u, f2v_t{wm[j], wl[j]});
   }
 
+  if (live == kGridLive) live = grid_live(a, seq_len_of(a, b));
   __shared__ int s_last;
   __builtin_amdgcn_s_waitcnt(0);  // this thread's partial stores are complete
   __syncthreads();

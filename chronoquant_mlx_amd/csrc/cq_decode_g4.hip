@@ -122,7 +122,11 @@ __global__ __launch_bounds__(kThreadsMfma) void decode_g4_kernel(DecodeArgs a) {
     __syncthreads();
   }
   for (int it = 0;; ++it) {
-    const int tid = thread_id();
+    // (balanced plan: the thread index is opaque per segment, so that the
+    // lane-derived addresses are computed inside the loop, not hoisted and
+    // kept live across the body)
+    const int tid = kBalanced ? thread_id() : (int)threadIdx.x;
+    __builtin_assume(tid >= 0 && tid < kThreadsMfma);
     const int lane = tid & 63, wave = tid >> 6;
     const int col = lane & 15, kg = lane >> 4;
     const int hq = col & 3;   // score layout: head of this lane's column
@@ -164,7 +168,7 @@ __global__ __launch_bounds__(kThreadsMfma) void decode_g4_kernel(DecodeArgs a) {
       t1 = min(T, t0 + a.split_len);
       if (split_is_empty(split, t0, T)) return;
       slot = split;
-      live = grid_live(a, T);
+      live = kGridLive;
     }
     const int64_t bh = (int64_t)b * a.H + h;
 
@@ -227,7 +231,8 @@ __global__ __launch_bounds__(kThreadsMfma) void decode_g4_kernel(DecodeArgs a) {
       }
     };
     // V anchor rows gv_base + 4kg + r of the chunk at c0, dims 8col .. 8col+7.
-    uint4 va[4] = {};
+    uint4 va[4];
+    if constexpr (kBalanced) va[0] = va[1] = va[2] = va[3] = uint4{0u, 0u, 0u, 0u};
     auto stage_va = [&](int c0) {
       const int nt = (int)max((int64_t)0, min((int64_t)kChunk, t1 - c0));
       const int gv_base = c0 >> lsv;
@@ -242,9 +247,11 @@ __global__ __launch_bounds__(kThreadsMfma) void decode_g4_kernel(DecodeArgs a) {
     // round trips overlap.
     int64_t c0l = t0 + (int64_t)wave * kChunk;
     const bool has_work = c0l < t1;
-    // (zero-initialised: left undefined on a segment without work, they would
-    // be carried from the previous segment and stay live across the body)
-    G4Buf bufA{}, bufB{};
+    // (balanced plan: zero-initialised; left undefined on a segment without
+    // work, they would be carried from the previous segment and stay live
+    // across the whole body)
+    G4Buf bufA, bufB;
+    if constexpr (kBalanced) bufA = bufB = G4Buf{};
     if (has_work) {
       stage((int)c0l, bufA);
       stage_va((int)c0l);

@@ -391,7 +391,7 @@ __global__ __launch_bounds__(kThreadsMfma) void decode_mfma_kernel(DecodeArgs a)
   }
   // code columns: x = 1032 + c (even nb, weight p s) or 1152 + 16c (odd nb,
   // weight p s / 16): subtract the constant parts
-  merge_and_finish(a, lds.mg, b, h, chunk, j0, gn, split, grid_live(a, T), m_run, l_run,
+  merge_and_finish(a, lds.mg, b, h, chunk, j0, gn, split, kGridLive, m_run, l_run,
                    [&](int nb, int r) {
     const float corr = (nb & 1) ? 1024.f * sw16[r] + 8.f * sw[r] : 1032.f * sw[r];
     return acc[nb][r] - corr;
@@ -515,7 +515,7 @@ __global__ __launch_bounds__(kThreadsMfma) void decode_plain_kernel(DecodeArgs a
     }
   }
   l_run = shfl_sum_kg(l_run);
-  merge_and_finish(a, lds.mg, b, h, chunk, j0, gn, split, grid_live(a, T), m_run, l_run,
+  merge_and_finish(a, lds.mg, b, h, chunk, j0, gn, split, kGridLive, m_run, l_run,
                    [&](int nb, int r) { return acc[nb][r]; });
 }
 

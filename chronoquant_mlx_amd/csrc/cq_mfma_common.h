@@ -152,7 +152,7 @@ template <typename OVal>
 __device__ __forceinline__ void merge_and_finish(const DecodeArgs &a, MergeScratch &M, int b,
                                                  int h, int chunk, int j0, int gn, int slot,
                                                  int live, float m_run, float l_run, OVal o_val) {
-  const int tid = thread_id(), lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int col = lane & 15, kg = lane >> 4;
   __syncthreads();  // wave scratch becomes the merge area
   if (kg == 0) {
