@@ -144,7 +144,8 @@ TRAFFIC_FILE = os.path.join(ROOT, "profiles", "decode_g4_c1_traffic.txt")
 def kernel_source_hash():
     import hashlib
     h = hashlib.sha256()
-    for f in ("cq_decode_g4.hip", "cq_mfma_common.h", "cq_decode_common.h"):
+    for f in ("cq_decode_g4.hip", "cq_mfma_common.h", "cq_decode_common.h", "cq_plan.h",
+              "cq_device.h"):
         with open(os.path.join(ROOT, "chronoquant_mlx_amd", "csrc", f), "rb") as fh:
             h.update(fh.read())
     return h.hexdigest()[:16]
