@@ -50,8 +50,10 @@ struct alignas(16) G4WaveScratch {
   uint2 pw[3][kG4][kChunk / 4 + 1];
 };
 
-// Per-workgroup LDS: q' of the group's heads in the unpack order of each
-// 8-dim slab, and the zero region the score product's off-block lanes read.
+// Per-workgroup LDS: q' of the group's heads in the order of the score
+// product's K operand (q[8 par + p][h]: the dims of parity par of slabs 2p and
+// 2p + 1, see unpack_pair), and the zero region the score product's off-block
+// lanes read.
 struct alignas(16) G4GroupScratch {
   h8_t q[16][kG4];
   h8_t pad[kG4];  // puts zero[m][h] 64 bytes off q[m][h]'s banks
@@ -68,6 +70,25 @@ union G4Lds {
   G4Stage s;
   MergeScratch mg;
 };
+
+// K operand of the score product from two code words (slabs 2p, 2p + 1).  A
+// nibble enters as an fp16 denormal: bits 0-3 and 4-7 of each 16-bit half
+// are read in place (n * 2^-24 and 16 n * 2^-24), bits 8-15 after one shift
+// by 8.  Parity 0 takes the low nibble of each byte, dims {0, 4, 2, 6} of a
+// slab in that order; parity 1 the high nibble, dims {1, 5, 3, 7} at 16 times
+// their value (the product's accumulator is scaled by 1/16).  Five VALU per
+// word for both parities.
+__device__ __forceinline__ h8_t unpack_pair(uint32_t wa, uint32_t wb, uint32_t ta, uint32_t tb,
+                                           uint32_t m) {
+  return h8_of(wa & m, ta & m, wb & m, tb & m);
+}
+// The same dims of an anchor row (fp16, natural order) for the anchor product:
+// u = dims 0..7 of slab 2p, v = of slab 2p + 1.
+__device__ __forceinline__ h8_t anchor_pair(uint4 u, uint4 v, bool odd) {
+  const uint32_t sel = odd ? 0x07060302u : 0x05040100u;
+  return h8_of(__builtin_amdgcn_perm(u.z, u.x, sel), __builtin_amdgcn_perm(u.w, u.y, sel),
+               __builtin_amdgcn_perm(v.z, v.x, sel), __builtin_amdgcn_perm(v.w, v.y, sel));
+}
 
 // The registers one chunk's loads land in.
 struct G4Buf {
@@ -206,7 +227,7 @@ __global__ __launch_bounds__(kThreadsMfma) void decode_g4_kernel(DecodeArgs a) {
         // slot -1 reads past the buffer: scale 0, codes 0
         cb.sk = bload16(r_sck, (uint32_t)slk * 2u);
         cb.sv = bload16(r_scv, (uint32_t)slv * 2u);
-  #pragma unroll
+#pragma unroll
         // the row's 4 quarters: each load touches every 64-byte row of the chunk
         // once, so these stay cacheable for the next three (no nt policy)
         for (int q = 0; q < 4; ++q) {
@@ -218,10 +239,10 @@ __global__ __launch_bounds__(kThreadsMfma) void decode_g4_kernel(DecodeArgs a) {
       wave_lds_sync();
       {
         const uint32_t row = ((uint32_t)min(gk_base + col, gk_last) * 256u + 64u * kg) | dead;
-  #pragma unroll
+#pragma unroll
         for (int kb = 0; kb < 4; ++kb) cb.ka[kb] = bload128(r_kfk, row + 16u * kb);
       }
-  #pragma unroll
+#pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int4 sl4 = *(const int4 *)&W.slot_v[16 * i + 4 * kg];
         cb.vw[i][0] = bload32(r_pkv, (uint32_t)sl4.x * 64u + 4u * col);
@@ -238,7 +259,7 @@ __global__ __launch_bounds__(kThreadsMfma) void decode_g4_kernel(DecodeArgs a) {
       const int gv_base = c0 >> lsv;
       const int gv_last = nt ? (c0 + nt - 1) >> lsv : gv_base;
       const uint32_t dead = nt ? 0u : 0x80000000u;
-  #pragma unroll
+#pragma unroll
       for (int r = 0; r < 4; ++r)
         va[r] = bload128(r_kfv, ((uint32_t)min(gv_base + 4 * kg + r, gv_last) * 256u + 16u * col) | dead);
     };
@@ -258,8 +279,8 @@ __global__ __launch_bounds__(kThreadsMfma) void decode_g4_kernel(DecodeArgs a) {
     }
 
     // ---- q table: q' = fp16(q * fp16(scale)) (bf16 queries: bf16(q * bf16(scale)))
-    // per (slab m, head), in the order {d0, d4, d1, d5, d2, d6, d3, d7} that
-    // unpack_k gives a code word's nibbles; heads >= gn are zero.
+    // per (parity, slab pair, head) in the order unpack_pair gives a code
+    // word pair's nibbles; heads >= gn are zero.
     if (tid < 64) {
       const int hh = tid >> 4, m = tid & 15;
       h8_t v = {};
@@ -269,11 +290,13 @@ __global__ __launch_bounds__(kThreadsMfma) void decode_g4_kernel(DecodeArgs a) {
             *(const uint4 *)((const uint16_t *)a.q + ((int64_t)b * a.nq + h * a.G + hh) * kD + 8 * m);
         const h8_t x = a.q_dtype == CQ_BF16 ? bf16x8_scaled_to_f16(raw, bf16_round(a.scale))
                                             : __builtin_bit_cast(h8_t, raw) * (_Float16)a.scale;
-        v = h8_t{x[0], x[4], x[1], x[5], x[2], x[6], x[3], x[7]};
-  #pragma unroll
+        v = x;
+#pragma unroll
         for (int e = 0; e < 8; ++e) part += (float)x[e];
       }
-      Gs.q[m][hh] = v;
+      // slab m is half m & 1 of pair m >> 1
+      ((h4_t *)&Gs.q[m >> 1][hh])[m & 1] = h4_t{v[0], v[4], v[2], v[6]};
+      ((h4_t *)&Gs.q[8 + (m >> 1)][hh])[m & 1] = h4_t{v[1], v[5], v[3], v[7]};
       part += __shfl_xor(part, 1, 64);
       part += __shfl_xor(part, 2, 64);
       part += __shfl_xor(part, 4, 64);
@@ -283,7 +306,7 @@ __global__ __launch_bounds__(kThreadsMfma) void decode_g4_kernel(DecodeArgs a) {
       (&Gs.zero[0][0])[tid - 64] = h8_t{};
     }
     __syncthreads();
-    // score-layout B operand of slab m: Gs.q[m][hq] on the diagonal blocks, else zeros
+    // score-layout B operand of (parity, pair): Gs.q[..][hq] on the diagonal blocks, else zeros
     const h8_t *qsrc = jb == kg ? &Gs.q[0][hq] : &Gs.zero[0][hq];
     // 16-head-layout B operand of the anchor product (q'^T, column = head)
     const h8_t *qcol = col < kG4 ? &Gs.q[0][col] : &Gs.zero[0][0];
@@ -298,7 +321,7 @@ __global__ __launch_bounds__(kThreadsMfma) void decode_g4_kernel(DecodeArgs a) {
     float w_run = 0.f;        // sum of fp16 p*s_v
     float x_run = 0.f;        // sum of fp16 p*s_v/16
     f4_t acc[8];
-  #pragma unroll
+#pragma unroll
     for (int nb = 0; nb < 8; ++nb) acc[nb] = f4_t{0.f, 0.f, 0.f, 0.f};
     const h2_t ones = {(_Float16)1.f, (_Float16)1.f};
     const h2_t sixteenth = {(_Float16)0.0625f, (_Float16)0.0625f};
@@ -312,37 +335,44 @@ __global__ __launch_bounds__(kThreadsMfma) void decode_g4_kernel(DecodeArgs a) {
       // block 0, whose m_run is head col's)
       {
         f4_t d = {0.f, 0.f, 0.f, 0.f};
-  #pragma unroll
-        for (int kb = 0; kb < 4; ++kb) d = mfma32(korder(cb.ka[kb]), qcol[(4 * kg + kb) * kG4], d);
+#pragma unroll
+        // product kb: lane group kg supplies parity kb & 1 of slabs 4kg + 2(kb >> 1), +1
+        for (int kb = 0; kb < 4; ++kb)
+          d = mfma32(anchor_pair(cb.ka[kb & 2], cb.ka[(kb & 2) + 1], kb & 1),
+                     qcol[(8 * (kb & 1) + 2 * kg + (kb >> 1)) * kG4], d);
         if (col < kG4) {
           const float mref = (m_run == -INFINITY) ? 0.f : m_run;
-  #pragma unroll
+#pragma unroll
           for (int r = 0; r < 4; ++r) W.qa[4 * kg + r][col] = __builtin_fmaf(d[r], kLog2e, -mref);
         }
       }
       wave_lds_sync();
 
       // ---- scores of tokens 16 jb + 4 kg + r, head hq (log2 units, minus mref) -------
-      // two independent accumulation chains; each group of 4 q slabs is read
-      // from LDS together
+      // two accumulation chains, one per parity (the odd one at 16x scale);
+      // the q' operands of a group of 4 slabs are read from LDS together
       f4_t d0 = {0.f, 0.f, 0.f, 0.f}, d1 = {0.f, 0.f, 0.f, 0.f};
-  #pragma unroll
+#pragma unroll
       for (int q = 0; q < 4; ++q) {
-        const h8_t b0 = qsrc[(4 * q + 0) * kG4], b1 = qsrc[(4 * q + 1) * kG4];
-        const h8_t b2 = qsrc[(4 * q + 2) * kG4], b3 = qsrc[(4 * q + 3) * kG4];
-        d0 = mfma32(unpack_k(cb.kr[q].x), b0, d0);
-        d1 = mfma32(unpack_k(cb.kr[q].y), b1, d1);
-        d0 = mfma32(unpack_k(cb.kr[q].z), b2, d0);
-        d1 = mfma32(unpack_k(cb.kr[q].w), b3, d1);
+        const h8_t e0 = qsrc[(2 * q) * kG4], o0 = qsrc[(8 + 2 * q) * kG4];
+        const h8_t e1 = qsrc[(2 * q + 1) * kG4], o1 = qsrc[(8 + 2 * q + 1) * kG4];
+        const uint4 w = cb.kr[q];
+        const uint32_t tx = w.x >> 8, ty = w.y >> 8, tz = w.z >> 8, tw = w.w >> 8;
+        d0 = mfma32(unpack_pair(w.x, w.y, tx, ty, 0x000F000Fu), e0, d0);
+        d1 = mfma32(unpack_pair(w.x, w.y, tx, ty, 0x00F000F0u), o0, d1);
+        d0 = mfma32(unpack_pair(w.z, w.w, tz, tw, 0x000F000Fu), e1, d0);
+        d1 = mfma32(unpack_pair(w.z, w.w, tz, tw, 0x00F000F0u), o1, d1);
       }
-      const f4_t d = d0 + d1;
+      f4_t d;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) d[r] = __builtin_fmaf(d1[r], 0.0625f, d0[r]);
       const int tb = 16 * jb + 4 * kg;
       const uint4 s4 = *(const uint4 *)&W.s16[sl][tb];
       const uint32_t sr[4] = {s4.x, s4.y, s4.z, s4.w};
       // the 4 tokens share one K anchor (stride >= 4, token groups aligned to 4)
       const float qa = W.qa[((c0 + tb) >> lsk) - gk_base][hq];
       float sc[4];
-  #pragma unroll
+#pragma unroll
       for (int r = 0; r < 4; ++r) {
         // log2e * s * (q'.c) with q'.c = 2^24 d - 8 sum(q')
         const float qc = __builtin_fmaf(d[r], kTwo24 * kLog2e, -s8l);
@@ -350,7 +380,7 @@ __global__ __launch_bounds__(kThreadsMfma) void decode_g4_kernel(DecodeArgs a) {
       }
       // Tokens past the end exist only in a split's last chunk (a uniform branch).
       if (cb.nt < kChunk) {
-  #pragma unroll
+#pragma unroll
         for (int r = 0; r < 4; ++r)
           if (tb + r >= cb.nt) sc[r] = -INFINITY;
       }
@@ -370,15 +400,15 @@ __global__ __launch_bounds__(kThreadsMfma) void decode_g4_kernel(DecodeArgs a) {
         l_run *= f;
         w_run *= f;
         x_run *= f;
-  #pragma unroll
+#pragma unroll
         for (int r = 0; r < 4; ++r) {
           // acc row 4kg + r holds head r (rows >= 4 repeat heads r, unused)
           const float fr = __shfl(f, r, 64);
-  #pragma unroll
+#pragma unroll
           for (int nb = 0; nb < 8; ++nb) acc[nb][r] *= fr;
         }
         const float shift = ((m_new == -INFINITY) ? 0.f : m_new) - mref;
-  #pragma unroll
+#pragma unroll
         for (int r = 0; r < 4; ++r) sc[r] -= shift;
         m_run = m_new;
       }
@@ -411,7 +441,7 @@ __global__ __launch_bounds__(kThreadsMfma) void decode_g4_kernel(DecodeArgs a) {
       // rows >= 4 repeat heads 0..3 and are never read).
       const int hr = col & 3;
       f4_t pg = {0.f, 0.f, 0.f, 0.f};  // P_g^T: lane holds groups 4kg+r, head col
-  #pragma unroll
+#pragma unroll
       for (int P = 0; P < 2; ++P) {
         const uint2 pa = W.pw[0][hr][8 * P + kg], pb = W.pw[0][hr][8 * P + 4 + kg];
         const uint2 wa = W.pw[1][hr][8 * P + kg], wb = W.pw[1][hr][8 * P + 4 + kg];
@@ -427,7 +457,7 @@ __global__ __launch_bounds__(kThreadsMfma) void decode_g4_kernel(DecodeArgs a) {
         pg = mfma32(h8_of(ea, ea, eb, eb), ap, pg);
         // V codes: B = 8 tokens x dim 8col + nb (nibble nb of word col)
         const int i0 = 2 * P, i1 = 2 * P + 1;
-  #pragma unroll
+#pragma unroll
         for (int k = 0; k < 4; ++k) {
           const uint32_t sel = (uint32_t)k | (0x0cu << 8) | ((uint32_t)(4 + k) << 16) | (0x0cu << 24);
           const uint32_t a01 = __builtin_amdgcn_perm(cb.vw[i0][1], cb.vw[i0][0], sel);
@@ -452,7 +482,7 @@ __global__ __launch_bounds__(kThreadsMfma) void decode_g4_kernel(DecodeArgs a) {
         const h2_t pl01 = h2_t{(_Float16)(pg[0] - (float)ph01.x), (_Float16)(pg[1] - (float)ph01.y)};
         const h2_t pl23 = h2_t{(_Float16)(pg[2] - (float)ph23.x), (_Float16)(pg[3] - (float)ph23.y)};
         const h8_t pa = h8_t{ph01.x, ph01.y, ph23.x, ph23.y, pl01.x, pl01.y, pl23.x, pl23.y};
-  #pragma unroll
+#pragma unroll
         for (int k = 0; k < 4; ++k) {
           const h4_t blo = rows_operand(va, k, false), bhi = rows_operand(va, k, true);
           acc[2 * k] = mfma32(pa, h8_t{blo[0], blo[1], blo[2], blo[3], blo[0], blo[1], blo[2], blo[3]},
@@ -481,14 +511,14 @@ __global__ __launch_bounds__(kThreadsMfma) void decode_g4_kernel(DecodeArgs a) {
     }
 
     // ---- totals of head hq: its 16 lanes hold disjoint tokens ---------------------------
-  #pragma unroll
+#pragma unroll
     for (int x = 4; x < 64; x *= 2) {
       l_run += __shfl_xor(l_run, x, 64);
       w_run += __shfl_xor(w_run, x, 64);
       x_run += __shfl_xor(x_run, x, 64);
     }
     float sw[4], sx[4];
-  #pragma unroll
+#pragma unroll
     for (int r = 0; r < 4; ++r) {
       sw[r] = __shfl(w_run, r, 64);  // lane r: head r
       sx[r] = __shfl(x_run, r, 64);
