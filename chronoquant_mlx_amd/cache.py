@@ -225,6 +225,13 @@ class ChronoQuantCache:
         need = _lib.load().cq_decode_workspace_size(B, H, n_q_heads, D, max(self._cap, 1))
         return _shared_workspace(self._device, need)
 
+    def _prefill_workspace(self, n_q_heads: int, n_q: int) -> torch.Tensor | None:
+        """Split-K workspace of cq_prefill_attn (the shared decode workspace,
+        grown when needed); None when the plan does not split."""
+        B, H, D = self._shape
+        need = _lib.load().cq_prefill_workspace_size(B, H, n_q_heads, n_q, max(self.offset, 1))
+        return _shared_workspace(self._device, need) if need else None
+
     # ------------------------------------------------------------------
     # append (cache.py:87-129, 198-215)
     # ------------------------------------------------------------------

@@ -341,7 +341,9 @@ struct SplitPlan {
 // Workgroups of `kernel` (launched with `threads` threads) that run at once on
 // the current device: CUs x maximum active blocks per CU, cached per device
 // under `slot` (one slot per decode kernel).
-enum ResidentSlot { kSlotGeneric = 0, kSlotMfmaPow2, kSlotMfma, kSlotPlain, kSlotG4, kSlotCount };
+enum ResidentSlot {
+  kSlotGeneric = 0, kSlotMfmaPow2, kSlotMfma, kSlotPlain, kSlotG4, kSlotPrefill, kSlotCount
+};
 int64_t resident_workgroups(const void *kernel, int threads, int slot);
 int64_t mfma_max_resident();     // max over the MFMA-file kernels
 int64_t decode_max_resident();   // max over every decode kernel

@@ -11,19 +11,28 @@
 // the P.V product.
 //
 // Workgroup = 4 waves = 64 query rows of one kv head: 64 / G positions x the
-// G q heads of the group (row R: position p0 + R / G, head R % G).  Per
-// 64-key block:
+// G q heads of the group (row R: position p0 + R / G, head R % G), over one
+// of nsplit contiguous pieces of its key range (split-K: with one workgroup
+// per 64 rows the grid is one workgroup per CU and one wave per SIMD, which
+// leaves every load's latency exposed; splits give each CU several
+// workgroups).  Per 64-key block:
 //   1. all 256 threads rebuild the K block (row-major) and the V block
 //      (transposed, dims x keys) in LDS with the reference's fp16 rounding;
 //   2. each wave computes S^T = K . Q^T for its 16 rows (v_mfma_f32_16x16x32_f16,
 //      4 key tiles x 4 K-steps), so a lane holds 16 scores of one row;
 //   3. online softmax in the log2 domain (lazy rescale beyond 2^8);
 //   4. O += P . V (8 dim tiles x 2 K-steps; two 16-key tiles per K=32 step).
+// With several splits each workgroup writes its rows' unnormalised (m, l, o)
+// to the workspace, and the last of a tile's splits to finish (a ticket on a
+// per-(sequence, kv head, tile) counter) merges them by log-sum-exp, as the
+// decode's split combine does.
 // Inside each 8-dim group the LDS blocks and the Q fragment use the dim order
 // {0,2,4,6,1,3,5,7}, the order the nibble unpack produces; the output store
 // undoes it.
 #include <hip/hip_runtime.h>
 #include <math.h>
+
+#include <algorithm>
 
 #include "cq_decode_common.h"
 
@@ -57,6 +66,10 @@ struct PrefillArgs {
   float scale;
   const uint16_t *q;  // [B][nq][n_q][D] fp16 or bf16
   uint16_t *out;      // [B][nq][n_q][D], the dtype of q
+  int nsplit, tiles;
+  float *part_ml;      // [B][nq][n_q][nsplit][2]  (m in log2 units, l)
+  float *part_acc;     // [B][nq][n_q][nsplit][D]  (real dim order)
+  uint32_t *counters;  // [B][H][tiles]
 };
 
 // bf16 q' = bf16(q * bf16(scale)) (one rounding of the exact fp32 product),
@@ -119,6 +132,106 @@ struct alignas(16) PrefillLds {
   uint16_t v[kD][kVStride];     // V block transposed, [dim (grouped order)][key]
 };
 
+// Split epilogue: this workgroup's rows' (m, l, o) go to the workspace with
+// device-scope stores; the last of the tile's nsplit workgroups to take a
+// ticket folds every row's partials by log-sum-exp, writes the output and
+// resets the counter.  Row R of the tile is position p0 + R / G, head R % G;
+// lane (col, kg) of wave w holds o of rows 16w + 4kg + r at grouped dims
+// 16dt + col, and m, l of row 16w + col.
+template <bool Bf16>
+__device__ __forceinline__ void split_epilogue(const PrefillArgs &a, int b, int h, int tile,
+                                               int split, int64_t p0, float m_run, float l_run,
+                                               const f4_t (&acc)[8]) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int col = lane & 15, kg = lane >> 4;
+  const int G = a.G, ns = a.nsplit;
+  const int64_t L = a.n_q;
+  const int perm8[8] = {0, 2, 4, 6, 1, 3, 5, 7};
+  const int64_t rows = (int64_t)a.B * a.nq * L;  // global rows (host-bounded below 2^31 / (ns D 4))
+  const __amdgpu_buffer_rsrc_t racc = make_rsrc(a.part_acc, (uint32_t)(rows * ns * kD * 4));
+  const __amdgpu_buffer_rsrc_t rml = make_rsrc(a.part_ml, (uint32_t)(rows * ns * 8));
+  auto grow = [&](int R) {  // global row of tile row R (valid position)
+    return (((int64_t)b * a.nq + h * G + R % G) * L + p0 + R / G);
+  };
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int R = 16 * wave + 4 * kg + r;
+    if (p0 + R / G < L) {
+      const uint32_t base = (uint32_t)((grow(R) * ns + split) * kD);
+#pragma unroll
+      for (int dt = 0; dt < 8; ++dt) {
+        const int gi = 16 * dt + col;
+        store_dev1(racc, 4u * (base + 8 * (gi >> 3) + perm8[gi & 7]), acc[dt][r]);
+      }
+    }
+  }
+  {
+    const int R = 16 * wave + col;
+    if (kg == 0 && p0 + R / G < L)
+      store_dev2(rml, (uint32_t)((grow(R) * ns + split) * 8), f2v_t{m_run, l_run});
+  }
+  __shared__ int s_last;
+  __builtin_amdgcn_s_waitcnt(0);  // this thread's partial stores are complete
+  __syncthreads();
+  uint32_t *ctr = a.counters + ((int64_t)b * a.H + h) * a.tiles + tile;
+  if (tid == 0) {
+    const uint32_t prev = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    s_last = (prev == (uint32_t)(ns - 1));
+  }
+  __syncthreads();
+  if (!s_last) return;
+  // fold: thread -> (row R, 4 real dims), all splits' loads issued before use
+  for (int u = tid; u < kRows * (kD / 4); u += kThreads) {
+    const int R = u / (kD / 4), d0 = 4 * (u % (kD / 4));
+    if (p0 + R / G >= L) continue;
+    const int64_t g = grow(R);
+    float M = -INFINITY, Ls = 0.f, o0 = 0.f, o1 = 0.f, o2 = 0.f, o3 = 0.f;
+    for (int s0 = 0; s0 < ns; s0 += 8) {
+      f2v_t ml[8];
+      f4v_t ov[8];
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        const uint32_t sp = (uint32_t)(g * ns + min(s0 + k, ns - 1));
+        ml[k] = load_dev2(rml, sp * 8u);
+        ov[k] = load_dev4(racc, (sp * (uint32_t)kD + (uint32_t)d0) * 4u);
+      }
+      float mb = M;
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        if (s0 + k >= ns) ml[k].x = -INFINITY;
+        mb = fmaxf(mb, ml[k].x);
+      }
+      const float mref = (mb == -INFINITY) ? 0.f : mb;
+      const float f = (M == -INFINITY) ? 0.f : fast_exp2(M - mref);
+      Ls *= f;
+      o0 *= f;
+      o1 *= f;
+      o2 *= f;
+      o3 *= f;
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        const float w = (ml[k].x == -INFINITY) ? 0.f : fast_exp2(ml[k].x - mref);
+        Ls += w * ml[k].y;
+        o0 += w * ov[k].x;
+        o1 += w * ov[k].y;
+        o2 += w * ov[k].z;
+        o3 += w * ov[k].w;
+      }
+      M = mb;
+    }
+    const float inv = Ls > 0.f ? 1.f / Ls : 0.f;
+    uint16_t *orow = a.out + g * kD + d0;
+    const float ov4[4] = {o0 * inv, o1 * inv, o2 * inv, o3 * inv};
+    uint16_t hv[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+      hv[c] = Bf16 ? f32_to_bf16_bits(ov4[c]) : __builtin_bit_cast(uint16_t, (_Float16)ov4[c]);
+    *(uint2 *)orow = uint2{(uint32_t)hv[0] | ((uint32_t)hv[1] << 16),
+                           (uint32_t)hv[2] | ((uint32_t)hv[3] << 16)};
+  }
+  if (tid == 0) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // Bf16: queries (and output) are bf16.  The reference then computes the
 // scores in fp32 (bf16 x fp16 promotes), so they are not rounded to fp16.
 template <bool Bf16>
@@ -127,8 +240,10 @@ __global__ __launch_bounds__(kThreads) void prefill_mfma_kernel(PrefillArgs a) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int col = lane & 15, kg = lane >> 4;
   const int h = blockIdx.y, b = blockIdx.z;
+  const int split = (int)(blockIdx.x % (unsigned)a.nsplit);
+  const int tile = (int)(blockIdx.x / (unsigned)a.nsplit);
   const int G = a.G, ppw = kRows / G;  // positions per workgroup
-  const int64_t p0 = (int64_t)blockIdx.x * ppw;
+  const int64_t p0 = (int64_t)tile * ppw;
   const int64_t bh = (int64_t)b * a.H + h;
   const int64_t T = a.T, L = a.n_q;
   const int64_t qbase = T - L;  // position of query 0
@@ -185,7 +300,9 @@ __global__ __launch_bounds__(kThreads) void prefill_mfma_kernel(PrefillArgs a) {
 
   const int64_t last_pos = min(p0 + ppw, L) - 1;
   const int64_t key_end = a.causal ? qbase + last_pos + 1 : T;  // keys [0, key_end)
-  const int64_t n_blocks = (key_end + kKeys - 1) / kKeys;
+  const int64_t n_all = (key_end + kKeys - 1) / kKeys;
+  // this split's blocks [kb_lo, kb_hi) of the tile's n_all (possibly none)
+  const int64_t kb_lo = split * n_all / a.nsplit, kb_hi = (split + 1) * n_all / a.nsplit;
 
   // Raw block data in registers: the next block's loads are issued right
   // after the current block has been rebuilt into LDS, so they arrive while
@@ -222,9 +339,9 @@ __global__ __launch_bounds__(kThreads) void prefill_mfma_kernel(PrefillArgs a) {
       v_an[j] = bload128(r_kfv, arow + 16u * vw);
     }
   };
-  if (n_blocks > 0) load_block(0);
+  if (kb_lo < kb_hi) load_block(kb_lo * kKeys);
 
-  for (int64_t kb = 0; kb < n_blocks; ++kb) {
+  for (int64_t kb = kb_lo; kb < kb_hi; ++kb) {
     const int64_t k0 = kb * kKeys;
     // ---- 1. rebuild the K and V blocks in LDS -----------------------------------
     {
@@ -252,7 +369,7 @@ __global__ __launch_bounds__(kThreads) void prefill_mfma_kernel(PrefillArgs a) {
             uint2{__builtin_amdgcn_perm(w1, w0, sel), __builtin_amdgcn_perm(w3, w2, sel)};
       }
     }
-    if (kb + 1 < n_blocks) load_block(k0 + kKeys);
+    if (kb + 1 < kb_hi) load_block(k0 + kKeys);
     __syncthreads();
 
     // ---- 2. S^T = K . Q^T: lane (col = row, kg) gets keys 16t + 4kg + r ---------
@@ -318,6 +435,10 @@ __global__ __launch_bounds__(kThreads) void prefill_mfma_kernel(PrefillArgs a) {
   l_run += __shfl_xor(l_run, 16, 64);
   l_run += __shfl_xor(l_run, 32, 64);
   const int perm8[8] = {0, 2, 4, 6, 1, 3, 5, 7};
+  if (a.nsplit > 1) {
+    split_epilogue<Bf16>(a, b, h, tile, split, p0, m_run, l_run, acc);
+    return;
+  }
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
     const int row = 16 * wave + 4 * kg + r;
@@ -343,9 +464,56 @@ __global__ __launch_bounds__(kThreads) void prefill_mfma_kernel(PrefillArgs a) {
 
 using namespace cq;
 
+namespace cq {
+namespace {
+
+// Split plan: enough key splits that the grid fills one resident generation
+// of workgroups (several per CU), at most kMaxPrefillSplits and no more than
+// the longest tile has key blocks; 1 when the workspace bounds are exceeded.
+constexpr int kMaxPrefillSplits = 16;
+
+struct PrefillPlan {
+  int tiles, nsplit;
+  size_t ws_bytes;  // 0: no workspace needed
+};
+
+PrefillPlan prefill_plan(int64_t B, int64_t H, int64_t G, int64_t n_q, int64_t T) {
+  PrefillPlan p;
+  const int64_t ppw = kRows / G;
+  p.tiles = (int)((n_q + ppw - 1) / ppw);
+  const int64_t groups = (int64_t)p.tiles * H * B;
+  const int64_t resident = resident_workgroups(
+      reinterpret_cast<const void *>(prefill_mfma_kernel<false>), kThreads, kSlotPrefill);
+  int64_t ns = (resident + groups - 1) / groups;
+  ns = std::min<int64_t>(ns, kMaxPrefillSplits);
+  ns = std::min<int64_t>(ns, (T + kKeys - 1) / kKeys);
+  const int64_t rows = B * H * G * n_q;
+  if (ns < 2 || B * H * p.tiles > kMaxCounters || rows * ns * kD * 4 >= ((int64_t)1 << 31)) ns = 1;
+  p.nsplit = (int)ns;
+  p.ws_bytes = ns > 1 ? kCounterRegion + round256((size_t)rows * ns * 8) +
+                            round256((size_t)rows * ns * kD * 4)
+                      : 0;
+  return p;
+}
+
+}  // namespace
+}  // namespace cq
+
+using namespace cq;
+
+extern "C" size_t cq_prefill_workspace_size(int32_t batch, int32_t n_kv_heads, int32_t n_q_heads,
+                                            int64_t n_q, int64_t seq_len) {
+  if (batch < 1 || n_kv_heads < 1 || n_q_heads < n_kv_heads || n_q_heads % n_kv_heads || n_q < 1)
+    return 0;
+  const int G = n_q_heads / n_kv_heads;
+  if (G > kRows || kRows % G) return 0;
+  return prefill_plan(batch, n_kv_heads, G, n_q, seq_len).ws_bytes;
+}
+
 extern "C" int cq_prefill_attn(const cq_cache_desc *cache, const void *q, int32_t q_dtype,
                                int32_t n_q_heads, int64_t n_q, float scale, int32_t causal,
-                               int64_t seq_len, void *out, cq_stream_t stream) {
+                               int64_t seq_len, void *out, void *workspace,
+                               size_t workspace_bytes, cq_stream_t stream) {
   int st = validate_cache(cache);
   if (st) return st;
   if (!q || !out) return CQ_ERR_ARG;
@@ -383,8 +551,22 @@ extern "C" int cq_prefill_attn(const cq_cache_desc *cache, const void *q, int32_
   a.scale = scale;
   a.q = (const uint16_t *)q;
   a.out = (uint16_t *)out;
-  const int ppw = kRows / G;
-  const dim3 grid((unsigned)((n_q + ppw - 1) / ppw), (unsigned)a.H, (unsigned)a.B);
+  const PrefillPlan plan = prefill_plan(a.B, a.H, G, n_q, seq_len);
+  a.tiles = plan.tiles;
+  a.nsplit = 1;
+  a.part_ml = a.part_acc = nullptr;
+  a.counters = nullptr;
+  if (plan.nsplit > 1 && workspace) {  // no workspace: one split per tile
+    if ((uintptr_t)workspace & 255) return CQ_ERR_ALIGN;
+    if (workspace_bytes < plan.ws_bytes) return CQ_ERR_WORKSPACE;
+    const int64_t rows = (int64_t)a.B * n_q_heads * n_q;
+    char *w = (char *)workspace;
+    a.counters = (uint32_t *)w;
+    a.part_ml = (float *)(w + kCounterRegion);
+    a.part_acc = (float *)(w + kCounterRegion + round256((size_t)rows * plan.nsplit * 8));
+    a.nsplit = plan.nsplit;
+  }
+  const dim3 grid((unsigned)(a.tiles * a.nsplit), (unsigned)a.H, (unsigned)a.B);
   if (q_dtype == CQ_BF16)
     prefill_mfma_kernel<true><<<grid, dim3(kThreads), 0, (hipStream_t)stream>>>(a);
   else

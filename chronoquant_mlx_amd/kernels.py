@@ -103,8 +103,11 @@ def chronoquant_prefill_kernel(q: torch.Tensor, cache, scale: float = 1.0,
     q = q.contiguous()
     B, nq, L, D = q.shape
     out = torch.empty_like(q)
+    ws = cache._prefill_workspace(nq, L)
+    ws_ptr, ws_bytes = (ws.data_ptr(), ws.numel()) if ws is not None else (None, 0)
     _lib.call("cq_prefill_attn", cache._descriptor(), q.data_ptr(), _lib.dtype_code(q.dtype), nq,
-              L, float(scale), int(bool(causal)), cache.offset, out.data_ptr(), _lib.stream_of(q))
+              L, float(scale), int(bool(causal)), cache.offset, out.data_ptr(), ws_ptr, ws_bytes,
+              _lib.stream_of(q))
     return out
 
 

@@ -174,10 +174,22 @@ int cq_fp16_decode_attn(const uint16_t *k, const uint16_t *v,
  * head_dim 128, n_q_heads / n_kv_heads dividing 64.  q_dtype CQ_F16 or
  * CQ_BF16 (bf16: q' = bf16(q * bf16(scale)) and fp32 scores, as the
  * reference's bf16 x fp16 promotion computes them; output bf16).
- * q, out: [B][n_q_heads][n_q][128] of q_dtype, 16-byte aligned. */
+ * q, out: [B][n_q_heads][n_q][128] of q_dtype, 16-byte aligned.
+ * workspace: caller-owned, zero-initialised device memory of at least
+ * cq_prefill_workspace_size(...) bytes, 256-byte aligned, for the split-K
+ * partials (the kernels leave its counter region zeroed again, so it is
+ * reused without clearing; it may be the decode workspace when large
+ * enough).  NULL: the key range is not split (slower, same result). */
 int cq_prefill_attn(const cq_cache_desc *cache, const void *q, int32_t q_dtype,
                     int32_t n_q_heads, int64_t n_q, float scale, int32_t causal,
-                    int64_t seq_len, void *out, cq_stream_t stream);
+                    int64_t seq_len, void *out, void *workspace, size_t workspace_bytes,
+                    cq_stream_t stream);
+
+/* Workspace bytes cq_prefill_attn needs for this shape on the current device
+ * (0: none; the key range is not split).  No counterpart in the reference
+ * (its fallback materialises the scores instead). */
+size_t cq_prefill_workspace_size(int32_t batch, int32_t n_kv_heads, int32_t n_q_heads,
+                                 int64_t n_q, int64_t seq_len);
 
 /* ---- Fused elementwise ops of the end-to-end decoder ------------------
  * No counterpart in the reference's own files: these are the roles of

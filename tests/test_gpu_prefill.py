@@ -123,3 +123,38 @@ def test_bf16_queries(causal):
     ck, cv = build_oracle(k[0], v[0], **params)
     ref = O.sdpa_fallback(qprime[0], ck.reconstruct(), cv.reconstruct(), 1.0, causal=causal)
     assert_close(out.float().cpu().numpy()[0], ref.astype(np.float64), what=f"causal={causal}")
+
+
+@pytest.mark.parametrize("bf16", [False, True])
+def test_split_keys_match_single_pass(bf16):
+    # The kernel splits each query tile's key range over several workgroups
+    # and merges their partials; without a workspace it runs one pass per
+    # tile.  Both must agree (they differ only in where the online softmax
+    # rounds its fp16 weights).
+    from chronoquant_mlx_amd import _lib
+    D, B, H, G, T, L = 128, 1, 8, 4, 3000, 512
+    params = dict(stride_k=64, stride_v=32, bits_v=3, dz_v=0.05)
+    k, v = _data(11, B, H, T, D)
+    q = np.random.default_rng(12).standard_normal((B, G * H, L, D)).astype(np.float16)
+    dt = torch.bfloat16 if bf16 else torch.float16
+    cache = build_gpu_cache(k, v, dtype=torch.float16, **params)
+    qt = to_gpu(q, dt).contiguous()
+    lib = _lib.load()
+    need = lib.cq_prefill_workspace_size(B, H, G * H, L, T)
+    assert need > 0, "this shape should split its keys"
+    ws = torch.zeros(need, dtype=torch.uint8, device="cuda")
+    outs = []
+    for w in (ws, None):
+        out = torch.empty_like(qt)
+        for _ in range(2):  # the second call reuses the counters of the first
+            _lib.call("cq_prefill_attn", cache._descriptor(), qt.data_ptr(), _lib.dtype_code(dt),
+                      G * H, L, D ** -0.5, 1, T, out.data_ptr(),
+                      None if w is None else w.data_ptr(), 0 if w is None else w.numel(),
+                      _lib.stream_of(qt))
+        outs.append(out.float().cpu().numpy())
+    torch.cuda.synchronize()
+    # (the oracle tests above run split plans too: their shapes leave the
+    # grid far below one resident generation)
+    tol = 8e-3 if bf16 else 2e-3
+    err = np.abs(outs[0] - outs[1]) - tol * np.abs(outs[1])
+    assert err.max() <= tol, err.max()
