@@ -127,6 +127,10 @@ __device__ __forceinline__ uint4 rebuild8(uint32_t cw, uint4 a, h2_t s2, uint32_
                as_u(a57 + c57 * s2)};
 }
 
+// Column (fp16 index) of 4-key group g in V^T row `row`: groups swapped in
+// pairs on rows 8..15 of every 16.
+__device__ __forceinline__ int vt_col(int row, int g) { return 4 * (g ^ ((row >> 3) & 1)); }
+
 struct alignas(16) PrefillLds {
   uint16_t k[kKeys][kKStride];  // K block, [key][dim (grouped order)]
   uint16_t v[kD][kVStride];     // V block transposed, [dim (grouped order)][key]
@@ -307,10 +311,19 @@ __global__ __launch_bounds__(kThreads) void prefill_mfma_kernel(PrefillArgs a) {
   // Raw block data in registers: the next block's loads are issued right
   // after the current block has been rebuilt into LDS, so they arrive while
   // the current block's products run.
-  //   K: thread -> key tid / 4, dims 32 (tid % 4) .. +31 (4 code words)
-  //   V: thread -> code word tid % 16 (dims 8w .. 8w+7), keys 4 (tid / 16) .. +3
-  const int kkey = tid >> 2, kqd = tid & 3;
-  const int vw = tid & 15, vkq = tid >> 4;
+  //   K: thread -> key (tid % 16) + 16 (tid / 64), dims 32 ((tid / 16) % 4) ..
+  //   +31 (4 code words): the lanes of one 16-byte LDS write phase are
+  //   consecutive keys of one quarter row (rows 68 dwords apart), which keeps
+  //   the writes conflict-free for 32- and 64-bank LDS alike.
+  //   V: thread -> code word tid / 16 (dims 8w .. 8w+7), keys 4 (tid % 16) .. +3.
+  //   The lanes of a 64-bit LDS write then cover keys 0..63 of V^T rows 8
+  //   apart (8 * 36 dwords = 32 banks): conflict-free.  (With the roles
+  //   swapped, lanes 8 rows apart hit 8 banks: an 8-way conflict on every
+  //   V^T write.)  V^T rows 8..15 of every 16 hold their 4-key groups
+  //   swapped in pairs (vt_col), so that the P.V reads of rows r and r + 8,
+  //   which share banks at 32 banks, touch different ones.
+  const int kkey = (tid & 15) | ((tid >> 6) << 4), kqd = (tid >> 4) & 3;
+  const int vw = tid >> 4, vkq = tid & 15;
   uint4 k_cw, k_an[4];
   uint32_t k_s;
   uint32_t v_cw[4], v_s[4];
@@ -365,7 +378,7 @@ __global__ __launch_bounds__(kThreads) void prefill_mfma_kernel(PrefillArgs a) {
         const uint32_t w1 = dw == 0 ? r[1].x : dw == 1 ? r[1].y : dw == 2 ? r[1].z : r[1].w;
         const uint32_t w2 = dw == 0 ? r[2].x : dw == 1 ? r[2].y : dw == 2 ? r[2].z : r[2].w;
         const uint32_t w3 = dw == 0 ? r[3].x : dw == 1 ? r[3].y : dw == 2 ? r[3].z : r[3].w;
-        *(uint2 *)&lds.v[8 * vw + i][4 * vkq] =
+        *(uint2 *)&lds.v[8 * vw + i][vt_col(8 * vw + i, vkq)] =
             uint2{__builtin_amdgcn_perm(w1, w0, sel), __builtin_amdgcn_perm(w3, w2, sel)};
       }
     }
@@ -423,8 +436,8 @@ __global__ __launch_bounds__(kThreads) void prefill_mfma_kernel(PrefillArgs a) {
                             as_u(pp[2 * P + 1][1]));
 #pragma unroll
       for (int dt = 0; dt < 8; ++dt) {
-        const uint2 v0 = *(const uint2 *)&lds.v[16 * dt + col][16 * (2 * P) + 4 * kg];
-        const uint2 v1 = *(const uint2 *)&lds.v[16 * dt + col][16 * (2 * P + 1) + 4 * kg];
+        const uint2 v0 = *(const uint2 *)&lds.v[16 * dt + col][vt_col(col, 8 * P + kg)];
+        const uint2 v1 = *(const uint2 *)&lds.v[16 * dt + col][vt_col(col, 8 * P + 4 + kg)];
         acc[dt] = mfma32(ap, h8_of(v0.x, v0.y, v1.x, v1.y), acc[dt]);
       }
     }
