@@ -10,13 +10,14 @@
 // the online (flash) form, with the weights rounded to fp16 where they enter
 // the P.V product.
 //
-// Workgroup = 4 waves = 64 query rows of one kv head: 64 / G positions x the
+// Workgroup = 8 waves = 128 query rows of one kv head: 128 / G positions x the
 // G q heads of the group (row R: position p0 + R / G, head R % G), over one
-// of nsplit contiguous pieces of its key range (split-K: with one workgroup
-// per 64 rows the grid is one workgroup per CU and one wave per SIMD, which
-// leaves every load's latency exposed; splits give each CU several
-// workgroups).  Per 64-key block:
-//   1. all 256 threads rebuild the K block (row-major) and the V block
+// of nsplit contiguous pieces of its key range (split-K: without splits a
+// chunk's grid is about one workgroup per CU, which leaves every load's
+// latency exposed; splits give each CU several).  128 rows share each
+// rebuilt block, so the rebuild costs half of what it would for 64.  Per
+// 64-key block:
+//   1. waves 0-3 rebuild the K block (row-major), waves 4-7 the V block
 //      (transposed, dims x keys) in LDS with the reference's fp16 rounding;
 //   2. each wave computes S^T = K . Q^T for its 16 rows (v_mfma_f32_16x16x32_f16,
 //      4 key tiles x 4 K-steps), so a lane holds 16 scores of one row;
@@ -46,9 +47,9 @@ typedef float f4_t __attribute__((ext_vector_type(4)));
 typedef int i4_t __attribute__((ext_vector_type(4)));
 
 constexpr int kD = 128;
-constexpr int kRows = 64;        // query rows per workgroup
+constexpr int kRows = 128;       // query rows per workgroup
 constexpr int kKeys = 64;        // keys per block
-constexpr int kThreads = 256;    // 4 waves
+constexpr int kThreads = 512;    // 8 waves: 16 rows each
 constexpr int kKStride = kD + 8;      // K block row stride (fp16 elements)
 constexpr int kVStride = kKeys + 8;   // V^T block row stride (fp16 elements)
 constexpr float kTau = 8.f;
@@ -238,7 +239,8 @@ __device__ __forceinline__ void split_epilogue(const PrefillArgs &a, int b, int 
 
 // Bf16: queries (and output) are bf16.  The reference then computes the
 // scores in fp32 (bf16 x fp16 promotes), so they are not rounded to fp16.
-template <bool Bf16>
+// Pow2: both strides are powers of two (token -> anchor / slot by shifts).
+template <bool Bf16, bool Pow2>
 __global__ __launch_bounds__(kThreads) void prefill_mfma_kernel(PrefillArgs a) {
   __shared__ PrefillLds lds;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -249,19 +251,9 @@ __global__ __launch_bounds__(kThreads) void prefill_mfma_kernel(PrefillArgs a) {
   const int G = a.G, ppw = kRows / G;  // positions per workgroup
   const int64_t p0 = (int64_t)tile * ppw;
   const int64_t bh = (int64_t)b * a.H + h;
-  const int64_t T = a.T, L = a.n_q;
-  const int64_t qbase = T - L;  // position of query 0
-  const int sk = a.stride[0], sv = a.stride[1];
-  const float isk = a.inv_stride[0], isv = a.inv_stride[1];
-
-  const __amdgpu_buffer_rsrc_t r_kfk = make_rsrc(a.kf[0] + bh * a.cap_kf[0] * kD, (uint32_t)(a.cap_kf[0] * kD * 2));
-  const __amdgpu_buffer_rsrc_t r_kfv = make_rsrc(a.kf[1] + bh * a.cap_kf[1] * kD, (uint32_t)(a.cap_kf[1] * kD * 2));
-  const __amdgpu_buffer_rsrc_t r_pkk = make_rsrc(a.pk[0] + bh * a.cap_pf[0] * 16, (uint32_t)(a.cap_pf[0] * 64));
-  const __amdgpu_buffer_rsrc_t r_pkv = make_rsrc(a.pk[1] + bh * a.cap_pf[1] * 16, (uint32_t)(a.cap_pf[1] * 64));
-  const __amdgpu_buffer_rsrc_t r_sck = make_rsrc(a.sc[0] + bh * a.cap_pf[0], (uint32_t)(a.cap_pf[0] * 2));
-  const __amdgpu_buffer_rsrc_t r_scv = make_rsrc(a.sc[1] + bh * a.cap_pf[1], (uint32_t)(a.cap_pf[1] * 2));
-  uint32_t magic;  // fp16 1024 in both halves, an opaque VGPR for the byte permutes
-  asm volatile("v_mov_b32 %0, 0x64006400" : "=v"(magic));
+  const int T = (int)a.T;  // < 2^24 (host-checked)
+  const int64_t L = a.n_q;
+  const int qbase = T - (int)L;  // position of query 0
 
   // ---- Q fragment: row (16 wave + col), dims of K-step s in the grouped
   // order; B operand of S^T = K . Q^T ----------------------------------------
@@ -295,7 +287,9 @@ __global__ __launch_bounds__(kThreads) void prefill_mfma_kernel(PrefillArgs a) {
     }
   }
   // causal limit of this lane's row (scores rows = lane col)
-  const int64_t lim = a.causal ? qbase + my_pos : T - 1;
+  const int lim = a.causal ? qbase + (int)my_pos : T - 1;
+  // every key of a block at or below lim_all is visible to every row of the tile
+  const int lim_all = a.causal ? qbase + (int)p0 : T - 1;
 
   float m_run = -INFINITY, l_run = 0.f;
   f4_t acc[8];
@@ -303,72 +297,93 @@ __global__ __launch_bounds__(kThreads) void prefill_mfma_kernel(PrefillArgs a) {
   for (int i = 0; i < 8; ++i) acc[i] = f4_t{0.f, 0.f, 0.f, 0.f};
 
   const int64_t last_pos = min(p0 + ppw, L) - 1;
-  const int64_t key_end = a.causal ? qbase + last_pos + 1 : T;  // keys [0, key_end)
-  const int64_t n_all = (key_end + kKeys - 1) / kKeys;
+  const int key_end = a.causal ? qbase + (int)last_pos + 1 : T;  // keys [0, key_end)
+  const int n_all = (key_end + kKeys - 1) / kKeys;
   // this split's blocks [kb_lo, kb_hi) of the tile's n_all (possibly none)
-  const int64_t kb_lo = split * n_all / a.nsplit, kb_hi = (split + 1) * n_all / a.nsplit;
+  const int kb_lo = split * n_all / a.nsplit, kb_hi = (split + 1) * n_all / a.nsplit;
 
-  // Raw block data in registers: the next block's loads are issued right
-  // after the current block has been rebuilt into LDS, so they arrive while
-  // the current block's products run.
-  //   K: thread -> key (tid % 16) + 16 (tid / 64), dims 32 ((tid / 16) % 4) ..
-  //   +31 (4 code words): the lanes of one 16-byte LDS write phase are
+  // Block staging: waves 0-3 load and rebuild the K block, waves 4-7 the V
+  // block, so that each thread holds one component's raw data in registers.
+  // The next block's loads are issued right after the current block has been
+  // rebuilt into LDS, so they arrive while the current block's products run.
+  //   K (thread st = tid): key (st % 16) + 16 (st / 64), dims 32 ((st / 16) % 4)
+  //   .. +31 (4 code words): the lanes of one 16-byte LDS write phase are
   //   consecutive keys of one quarter row (rows 68 dwords apart), which keeps
   //   the writes conflict-free for 32- and 64-bank LDS alike.
-  //   V: thread -> code word tid / 16 (dims 8w .. 8w+7), keys 4 (tid % 16) .. +3.
-  //   The lanes of a 64-bit LDS write then cover keys 0..63 of V^T rows 8
-  //   apart (8 * 36 dwords = 32 banks): conflict-free.  (With the roles
-  //   swapped, lanes 8 rows apart hit 8 banks: an 8-way conflict on every
-  //   V^T write.)  V^T rows 8..15 of every 16 hold their 4-key groups
-  //   swapped in pairs (vt_col), so that the P.V reads of rows r and r + 8,
-  //   which share banks at 32 banks, touch different ones.
-  const int kkey = (tid & 15) | ((tid >> 6) << 4), kqd = (tid >> 4) & 3;
-  const int vw = tid >> 4, vkq = tid & 15;
-  uint4 k_cw, k_an[4];
-  uint32_t k_s;
-  uint32_t v_cw[4], v_s[4];
-  uint4 v_an[4];
-  auto load_block = [&](int64_t k0) {
-    {
-      const int t = (int)(k0 + kkey);
-      const bool in = t < T;
-      const int g = div_stride(t, sk, isk);
-      const int slot = (in && t != g * sk) ? t - g - 1 : -1;  // -1: I-frame / past the end
-      const uint32_t arow = in ? (uint32_t)g * 256u : 0x80000000u;
-      k_s = bload16(r_sck, (uint32_t)slot * 2u);
-      k_cw = bload128(r_pkk, (uint32_t)slot * 64u + 16u * kqd);
-#pragma unroll
-      for (int j = 0; j < 4; ++j) k_an[j] = bload128(r_kfk, arow + 64u * kqd + 16u * j);
+  //   V (thread st = tid - 256): code word st / 16 (dims 8w .. 8w+7), keys
+  //   4 (st % 16) .. +3.  The lanes of a 64-bit LDS write then cover keys
+  //   0..63 of V^T rows 8 apart (8 * 36 dwords = 32 banks): conflict-free.
+  //   (With the roles swapped, lanes 8 rows apart hit 8 banks: an 8-way
+  //   conflict on every V^T write.)  V^T rows 8..15 of every 16 hold their
+  //   4-key groups swapped in pairs (vt_col), so that the P.V reads of rows r
+  //   and r + 8, which share banks at 32 banks, touch different ones.
+  const bool kside = tid < kThreads / 2;  // wave-uniform
+  const int st = tid & (kThreads / 2 - 1);
+  const int c = kside ? 0 : 1;
+  const int stride = a.stride[c];
+  const float istride = a.inv_stride[c];
+  const int lstride = __builtin_ctz(stride), mstride = stride - 1;
+  const __amdgpu_buffer_rsrc_t r_kf = make_rsrc(a.kf[c] + bh * a.cap_kf[c] * kD, (uint32_t)(a.cap_kf[c] * kD * 2));
+  const __amdgpu_buffer_rsrc_t r_pk = make_rsrc(a.pk[c] + bh * a.cap_pf[c] * 16, (uint32_t)(a.cap_pf[c] * 64));
+  const __amdgpu_buffer_rsrc_t r_sc = make_rsrc(a.sc[c] + bh * a.cap_pf[c], (uint32_t)(a.cap_pf[c] * 2));
+  const int kkey = (st & 15) | ((st >> 6) << 4), kqd = (st >> 4) & 3;
+  const int vw = st >> 4, vkq = st & 15;
+  uint32_t magic;  // fp16 1024 in both halves, an opaque VGPR for the byte permutes
+  asm volatile("v_mov_b32 %0, 0x64006400" : "=v"(magic));
+  uint32_t r_cw[4], r_s[4];  // K: code words of the quarter row, scale in r_s[0]
+  uint4 r_an[4];             //    anchor dims 32 kqd + 8j ..; V: per key j
+  // token t -> anchor index g (-1 past the end) and P-frame slot (-1:
+  // I-frame or past the end)
+  auto locate = [&](int t, int &g, int &slot) {
+    const bool in = t < T;
+    if (Pow2) {
+      g = t >> lstride;
+      slot = (in && (t & mstride)) ? t - g - 1 : -1;
+    } else {
+      g = div_stride(t, stride, istride);
+      slot = (in && t != g * stride) ? t - g - 1 : -1;
     }
+    if (!in) g = -1;
+  };
+  auto load_block = [&](int k0) {
+    if (kside) {
+      int g, slot;
+      locate(k0 + kkey, g, slot);
+      const uint32_t arow = g >= 0 ? (uint32_t)g * 256u : 0x80000000u;
+      r_s[0] = bload16(r_sc, (uint32_t)slot * 2u);
+      const uint4 cw = bload128(r_pk, (uint32_t)slot * 64u + 16u * kqd);
+      r_cw[0] = cw.x;
+      r_cw[1] = cw.y;
+      r_cw[2] = cw.z;
+      r_cw[3] = cw.w;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int t = (int)(k0 + 4 * vkq + j);
-      const bool in = t < T;
-      const int g = div_stride(t, sv, isv);
-      const int slot = (in && t != g * sv) ? t - g - 1 : -1;
-      const uint32_t arow = in ? (uint32_t)g * 256u : 0x80000000u;
-      v_s[j] = bload16(r_scv, (uint32_t)slot * 2u);
-      v_cw[j] = bload32(r_pkv, (uint32_t)slot * 64u + 4u * vw);
-      v_an[j] = bload128(r_kfv, arow + 16u * vw);
+      for (int j = 0; j < 4; ++j) r_an[j] = bload128(r_kf, arow + 64u * kqd + 16u * j);
+    } else {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        int g, slot;
+        locate(k0 + 4 * vkq + j, g, slot);
+        const uint32_t arow = g >= 0 ? (uint32_t)g * 256u : 0x80000000u;
+        r_s[j] = bload16(r_sc, (uint32_t)slot * 2u);
+        r_cw[j] = bload32(r_pk, (uint32_t)slot * 64u + 4u * vw);
+        r_an[j] = bload128(r_kf, arow + 16u * vw);
+      }
     }
   };
   if (kb_lo < kb_hi) load_block(kb_lo * kKeys);
 
-  for (int64_t kb = kb_lo; kb < kb_hi; ++kb) {
-    const int64_t k0 = kb * kKeys;
-    // ---- 1. rebuild the K and V blocks in LDS -----------------------------------
-    {
-      const h2_t s2 = as_h2(k_s * 0x10001u);
+  for (int kb = kb_lo; kb < kb_hi; ++kb) {
+    const int k0 = kb * kKeys;
+    // ---- 1. rebuild the K (waves 0-3) or V (waves 4-7) block in LDS ------------
+    if (kside) {
+      const h2_t s2 = as_h2(r_s[0] * 0x10001u);
       uint4 *dst = (uint4 *)&lds.k[kkey][32 * kqd];
-      dst[0] = rebuild8(k_cw.x, k_an[0], s2, magic);
-      dst[1] = rebuild8(k_cw.y, k_an[1], s2, magic);
-      dst[2] = rebuild8(k_cw.z, k_an[2], s2, magic);
-      dst[3] = rebuild8(k_cw.w, k_an[3], s2, magic);
-    }
-    {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) dst[j] = rebuild8(r_cw[j], r_an[j], s2, magic);
+    } else {
       uint4 r[4];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) r[j] = rebuild8(v_cw[j], v_an[j], as_h2(v_s[j] * 0x10001u), magic);
+      for (int j = 0; j < 4; ++j) r[j] = rebuild8(r_cw[j], r_an[j], as_h2(r_s[j] * 0x10001u), magic);
       // transpose: row 8w + i of V^T holds grouped-order dim i of the 4 keys
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
@@ -387,7 +402,6 @@ __global__ __launch_bounds__(kThreads) void prefill_mfma_kernel(PrefillArgs a) {
 
     // ---- 2. S^T = K . Q^T: lane (col = row, kg) gets keys 16t + 4kg + r ---------
     float sc[4][4];
-    float mx = -INFINITY;
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
       f4_t d = {0.f, 0.f, 0.f, 0.f};
@@ -398,13 +412,23 @@ __global__ __launch_bounds__(kThreads) void prefill_mfma_kernel(PrefillArgs a) {
       }
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const int64_t key = k0 + 16 * t + 4 * kg + r;
         // fp16 q: scores rounded to fp16 like the fallback's fp16 matmul
         const float sv16 = Bf16 ? d[r] : (float)(_Float16)d[r];
-        sc[t][r] = key <= lim ? sv16 * kLog2e : -INFINITY;
-        mx = fmaxf(mx, sc[t][r]);
+        sc[t][r] = sv16 * kLog2e;
       }
     }
+    // Keys past lim_all exist only in a tile's last blocks (a uniform branch).
+    if (k0 + kKeys - 1 > lim_all) {
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          if (k0 + 16 * t + 4 * kg + r > lim) sc[t][r] = -INFINITY;
+    }
+    float mx = -INFINITY;
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+      mx = fmaxf(mx, fmaxf(fmaxf(sc[t][0], sc[t][1]), fmaxf(sc[t][2], sc[t][3])));
     // ---- 3. online softmax (row max over the 4 lane groups of the column) -------
     mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
     mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
@@ -496,7 +520,7 @@ PrefillPlan prefill_plan(int64_t B, int64_t H, int64_t G, int64_t n_q, int64_t T
   p.tiles = (int)((n_q + ppw - 1) / ppw);
   const int64_t groups = (int64_t)p.tiles * H * B;
   const int64_t resident = resident_workgroups(
-      reinterpret_cast<const void *>(prefill_mfma_kernel<false>), kThreads, kSlotPrefill);
+      reinterpret_cast<const void *>(prefill_mfma_kernel<false, true>), kThreads, kSlotPrefill);
   int64_t ns = (resident + groups - 1) / groups;
   ns = std::min<int64_t>(ns, kMaxPrefillSplits);
   ns = std::min<int64_t>(ns, (T + kKeys - 1) / kKeys);
@@ -580,9 +604,15 @@ extern "C" int cq_prefill_attn(const cq_cache_desc *cache, const void *q, int32_
     a.nsplit = plan.nsplit;
   }
   const dim3 grid((unsigned)(a.tiles * a.nsplit), (unsigned)a.H, (unsigned)a.B);
-  if (q_dtype == CQ_BF16)
-    prefill_mfma_kernel<true><<<grid, dim3(kThreads), 0, (hipStream_t)stream>>>(a);
-  else
-    prefill_mfma_kernel<false><<<grid, dim3(kThreads), 0, (hipStream_t)stream>>>(a);
+  const bool pow2 = ((a.stride[0] & (a.stride[0] - 1)) | (a.stride[1] & (a.stride[1] - 1))) == 0;
+  const dim3 blk(kThreads);
+  const hipStream_t s = (hipStream_t)stream;
+  if (q_dtype == CQ_BF16) {
+    if (pow2) prefill_mfma_kernel<true, true><<<grid, blk, 0, s>>>(a);
+    else prefill_mfma_kernel<true, false><<<grid, blk, 0, s>>>(a);
+  } else {
+    if (pow2) prefill_mfma_kernel<false, true><<<grid, blk, 0, s>>>(a);
+    else prefill_mfma_kernel<false, false><<<grid, blk, 0, s>>>(a);
+  }
   return hipGetLastError() == hipSuccess ? CQ_OK : CQ_ERR_LAUNCH;
 }
