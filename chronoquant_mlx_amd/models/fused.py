@@ -18,6 +18,25 @@ def _check_weight(w: torch.Tensor, x: torch.Tensor, n: int, what: str) -> None:
         raise ValueError(f"{what}: weight must be a contiguous [{n}] {x.dtype} tensor on x's device")
 
 
+def linear(x: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
+    """x @ weight.T (a bias-free torch Linear).  One input row of fp16/bf16
+    (a decode step) runs cq_gemv, which streams the weight once; anything
+    else runs torch's GEMM."""
+    K = x.shape[-1]
+    if (x.numel() != K or x.dtype not in (torch.float16, torch.bfloat16)
+            or weight.dtype != x.dtype or K % 8 or not weight.is_contiguous()
+            or weight.data_ptr() % 16 or x.device != weight.device or x.device.type != "cuda"):
+        return torch.nn.functional.linear(x, weight)
+    x = x.contiguous()
+    if x.data_ptr() % 16:
+        x = x.clone()
+    N = weight.shape[0]
+    y = torch.empty(*x.shape[:-1], N, dtype=x.dtype, device=x.device)
+    _lib.call("cq_gemv", weight.data_ptr(), x.data_ptr(), y.data_ptr(), N, K,
+              _lib.dtype_code(x.dtype), _lib.stream_of(x))
+    return y
+
+
 def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor:
     """x * rsqrt(mean(x^2, -1) + eps) * weight over the last dim."""
     _lib.require_gpu(x)

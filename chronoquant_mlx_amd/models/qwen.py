@@ -10,9 +10,10 @@ dims, SwiGLU MLP, untied LM head) whose attention calls this module's
 `scaled_dot_product_attention`, the binding apply() replaces.  Keys are
 cached after RoPE, as in mlx_lm.
 
-Dense projections are plain torch matmuls (hipBLASLt), with the q/k/v and
-the gate/up projections each fused into one matrix (rows: query heads, key
-heads, value heads; gate, up).  The attention and the KV cache are the
+Dense projections are torch matmuls (hipBLASLt), with the q/k/v and the
+gate/up projections each fused into one matrix (rows: query heads, key
+heads, value heads; gate, up); with FUSED_OPS a single input row (a decode
+step) takes the library's GEMV, which streams each weight once.  The attention and the KV cache are the
 library's, and so are the elementwise ops when FUSED_OPS is set (the
 default): residual add + RMSNorm, the QKV split with q/k RMSNorm and RoPE,
 and the SwiGLU gate (models/fused.py).  FUSED_OPS = False runs the same
@@ -103,7 +104,7 @@ class Attention(nn.Module):
 
     def forward(self, x, positions, mask, cache):
         B, L, _ = x.shape
-        qkv = self.qkv_proj(x)
+        qkv = fused.linear(x, self.qkv_proj.weight) if FUSED_OPS else self.qkv_proj(x)
         if FUSED_OPS:
             q, k, v = fused.qkv_norm_rope(qkv, self.nh, self.nkv, self.q_norm.weight,
                                           self.k_norm.weight, self.rope.cos, self.rope.sin,
@@ -113,7 +114,8 @@ class Attention(nn.Module):
         keys, values = cache.update_and_fetch(k, v)
         out = scaled_dot_product_attention(q, keys, values, cache=cache, scale=self.scale,
                                            mask=mask)
-        return self.o_proj(out.transpose(1, 2).reshape(B, L, self.nh * self.hd))
+        out = out.transpose(1, 2).reshape(B, L, self.nh * self.hd)
+        return fused.linear(out, self.o_proj.weight) if FUSED_OPS else self.o_proj(out)
 
 
 class MLP(nn.Module):
@@ -124,9 +126,10 @@ class MLP(nn.Module):
         self.down_proj = nn.Linear(a.intermediate_size, a.hidden_size, bias=False)
 
     def forward(self, x):
-        gu = self.gate_up_proj(x)
         if FUSED_OPS:
-            return self.down_proj(fused.silu_mul(gu))
+            gu = fused.linear(x, self.gate_up_proj.weight)
+            return fused.linear(fused.silu_mul(gu), self.down_proj.weight)
+        gu = self.gate_up_proj(x)
         return self.down_proj(F.silu(gu[..., :self.inter]) * gu[..., self.inter:])
 
 
@@ -181,7 +184,7 @@ class Model(nn.Module):
             if last_only and i + 1 == n:
                 m, h = m[:, -1:], h[:, -1:]
             x, y = fused.add_rms_norm(m, h, w_next, eps)
-        return self.lm_head(y)
+        return fused.linear(y, self.lm_head.weight)
 
 
 def random_model(args: ModelArgs | None = None, device="cuda", dtype=torch.bfloat16,

@@ -199,6 +199,13 @@ size_t cq_prefill_workspace_size(int32_t batch, int32_t n_kv_heads, int32_t n_q_
  * CQ_BF16 or CQ_F32 for every tensor argument except the fp32 rotary
  * tables; math in fp32, one rounding per stored value. */
 
+/* y = W x for one input row (a Linear layer with M = 1: the decoder's
+ * projections in a decode step).  W: [n][k] row-major (a torch Linear
+ * weight), x: [k], y: [n]; dtype CQ_F16 or CQ_BF16, fp32 accumulation, one
+ * rounding per output.  k % 8 == 0, W and x 16-byte aligned. */
+int cq_gemv(const void *w, const void *x, void *y, int64_t n, int32_t k, int32_t dtype,
+            cq_stream_t stream);
+
 /* y[r] = x[r] * rsqrt(mean(x[r]^2) + eps) * w, rows of dim elements. */
 int cq_rms_norm(const void *x, const void *w, void *y, int64_t rows, int32_t dim,
                 float eps, int32_t dtype, cq_stream_t stream);

@@ -1,5 +1,5 @@
-"""GPU parity of the decoder's fused elementwise kernels (cq_rms_norm,
-cq_add_rms_norm, cq_qkv_norm_rope, cq_silu_mul) against torch fp32
+"""GPU parity of the decoder's fused kernels (cq_rms_norm, cq_add_rms_norm,
+cq_qkv_norm_rope, cq_silu_mul, and the one-row projection cq_gemv) against torch fp32
 statements of the same math, rounded once to the tensor dtype, plus closed
 forms: a constant row normalises to the weight, position 0 is the identity
 rotation, a rotation keeps each pair's norm, out-of-range positions give NaN.
@@ -156,6 +156,27 @@ def test_silu_mul(dtype, rows, n):
     gu = (torch.randn(rows, 2 * n, device="cuda", generator=g) * 3).to(dtype)
     ref = F.silu(gu[:, :n]) * gu[:, n:]
     _assert_ulp(fused.silu_mul(gu), ref, f"silu {rows}x{n}")
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("n,k", [(4096, 4096), (6144, 4096), (4096, 12288), (13, 72), (9, 520),
+                                 (1000, 4104)])
+def test_gemv(dtype, n, k):
+    # One input row through cq_gemv against the fp32 product rounded once.
+    # The fp32 sums differ only in order (k terms), so the rounded results
+    # agree to one ulp of the result plus the fp32 summation error bound.
+    from chronoquant_mlx_amd.models import fused
+    g = torch.Generator(device="cuda").manual_seed(n * 7 + k)
+    w = (torch.randn(n, k, device="cuda", generator=g) * 0.02).to(dtype)
+    x = torch.randn(1, 1, k, device="cuda", generator=g).to(dtype)
+    got = fused.linear(x, w)
+    exact = x.float().reshape(1, k) @ w.float().t()
+    ref = exact.to(dtype).reshape(1, 1, n)
+    mag = (x.float().abs().reshape(1, k) @ w.float().abs().t()).reshape(1, 1, n)
+    err = (got.float() - ref.float()).abs()
+    tol = ULP[dtype] * ref.float().abs() + k * 2.0 ** -23 * mag + TINY[dtype]
+    assert (err <= tol).all(), (err - tol).max().item()
+    assert got.shape == (1, 1, n) and got.dtype == dtype
 
 
 def test_argument_errors():
