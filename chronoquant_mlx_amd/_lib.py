@@ -77,6 +77,8 @@ SIGNATURES = {
     "cq_prefill_attn": ([_DESC, _P, _I32, _I32, _I64, _F, _I32, _I64, _P, _P, _SZ, _P], _I32),
     "cq_prefill_workspace_size": ([_I32, _I32, _I32, _I64, _I64], _SZ),
     "cq_gemv": ([_P, _P, _P, _I64, _I32, _I32, _P], _I32),
+    "cq_gemv_rms_norm": ([_P, _P, _P, _P, _F, _P, _P, _I64, _I32, _I32, _P], _I32),
+    "cq_gemv_silu": ([_P, _P, _P, _I64, _I32, _I32, _P], _I32),
     "cq_rms_norm": ([_P, _P, _P, _I64, _I32, _F, _I32, _P], _I32),
     "cq_add_rms_norm": ([_P, _P, _P, _P, _P, _I64, _I32, _F, _I32, _P], _I32),
     "cq_qkv_norm_rope": ([_P, _P, _P, _P, _P, _P, _P, _P, _I64, _P, _I64, _I32, _I64, _I32, _I32,

@@ -37,6 +37,55 @@ def linear(x: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
     return y
 
 
+def _one_row_ok(x: torch.Tensor, weight: torch.Tensor, k: int) -> bool:
+    return (x.numel() == k and x.dtype in (torch.float16, torch.bfloat16) and weight.dtype == x.dtype
+            and k % 8 == 0 and weight.is_contiguous() and weight.data_ptr() % 16 == 0
+            and x.is_contiguous() and x.data_ptr() % 16 == 0 and x.device == weight.device
+            and x.device.type == "cuda")
+
+
+def linear_rms_norm(x: torch.Tensor, residual: torch.Tensor | None, norm_weight: torch.Tensor,
+                    eps: float, weight: torch.Tensor, want_h: bool = False):
+    """One row: h = x + residual (or x), y = rms_norm(h, norm_weight) @ weight.T
+    in one launch (cq_gemv_rms_norm).  Returns (y, h) with h None unless
+    want_h (which needs a residual)."""
+    K = x.shape[-1]
+    ok = (_one_row_ok(x, weight, K) and K <= 8192 and norm_weight.dtype == x.dtype
+          and norm_weight.is_contiguous() and norm_weight.data_ptr() % 16 == 0
+          and (residual is None or (residual.is_contiguous() and residual.dtype == x.dtype
+                                    and residual.numel() == K and residual.data_ptr() % 16 == 0)))
+    if not ok:
+        h = x if residual is None else None
+        if residual is not None:
+            h, xn = add_rms_norm(x, residual, norm_weight, eps)
+        else:
+            xn = rms_norm(x, norm_weight, eps)
+        return linear(xn, weight), (h if want_h else None)
+    if want_h and residual is None:
+        raise ValueError("linear_rms_norm: want_h needs a residual")
+    N = weight.shape[0]
+    y = torch.empty(*x.shape[:-1], N, dtype=x.dtype, device=x.device)
+    h = torch.empty_like(x) if want_h else None
+    _lib.call("cq_gemv_rms_norm", weight.data_ptr(), x.data_ptr(),
+              None if residual is None else residual.data_ptr(), norm_weight.data_ptr(),
+              float(eps), None if h is None else h.data_ptr(), y.data_ptr(), N, K,
+              _lib.dtype_code(x.dtype), _lib.stream_of(x))
+    return y, h
+
+
+def linear_silu(gu: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
+    """One row: silu_mul(gu) @ weight.T in one launch (cq_gemv_silu)."""
+    K = gu.shape[-1] // 2
+    if not (_one_row_ok(gu.reshape(-1)[:K], weight, K) and gu.numel() == 2 * K
+            and gu.is_contiguous()):
+        return linear(silu_mul(gu), weight)
+    N = weight.shape[0]
+    y = torch.empty(*gu.shape[:-1], N, dtype=gu.dtype, device=gu.device)
+    _lib.call("cq_gemv_silu", weight.data_ptr(), gu.data_ptr(), y.data_ptr(), N, K,
+              _lib.dtype_code(gu.dtype), _lib.stream_of(gu))
+    return y
+
+
 def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor:
     """x * rsqrt(mean(x^2, -1) + eps) * weight over the last dim."""
     _lib.require_gpu(x)

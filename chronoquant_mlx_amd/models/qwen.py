@@ -102,9 +102,12 @@ class Attention(nn.Module):
         v = qkv[..., nq + nk:].reshape(B, L, self.nkv, self.hd).transpose(1, 2)
         return self.rope(q, positions), self.rope(k, positions), v
 
-    def forward(self, x, positions, mask, cache):
-        B, L, _ = x.shape
-        qkv = fused.linear(x, self.qkv_proj.weight) if FUSED_OPS else self.qkv_proj(x)
+    def forward(self, x, positions, mask, cache, qkv=None):
+        """qkv: the fused QKV projection of x when the caller computed it
+        (then x is unused)."""
+        if qkv is None:
+            qkv = fused.linear(x, self.qkv_proj.weight) if FUSED_OPS else self.qkv_proj(x)
+        B, L, _ = qkv.shape
         if FUSED_OPS:
             q, k, v = fused.qkv_norm_rope(qkv, self.nh, self.nkv, self.q_norm.weight,
                                           self.k_norm.weight, self.rope.cos, self.rope.sin,
@@ -166,6 +169,8 @@ class Model(nn.Module):
             positions = torch.arange(off, off + L, device=tokens.device)
         mask = "causal" if L > 1 else None
         x = self.embed_tokens(tokens)
+        if FUSED_OPS and B * L == 1:
+            return self._forward_one(x, positions, cache)
         if not FUSED_OPS:
             for layer, c in zip(self.layers, cache):
                 x = layer(x, positions, mask, c)
@@ -185,6 +190,27 @@ class Model(nn.Module):
                 m, h = m[:, -1:], h[:, -1:]
             x, y = fused.add_rms_norm(m, h, w_next, eps)
         return fused.linear(y, self.lm_head.weight)
+
+    def _forward_one(self, x, positions, cache):
+        """One token (a decode step) with the fused ops: every RMSNorm and
+        residual add runs inside the projection that consumes it
+        (fused.linear_rms_norm) and the SwiGLU gate inside the down projection
+        (fused.linear_silu).  The residual stream: x_i (layer input), h_i =
+        x_i + attn_i, x_{i+1} = h_i + mlp_i."""
+        eps = self.norm.eps
+        inp, res = x, None  # x_i = inp + res (res None: x_i = inp)
+        for layer, c in zip(self.layers, cache):
+            attn, mlp = layer.self_attn, layer.mlp
+            qkv, xi = fused.linear_rms_norm(inp, res, layer.input_layernorm.weight, eps,
+                                            attn.qkv_proj.weight, want_h=res is not None)
+            if res is None:
+                xi = inp
+            a = attn(None, positions, None, c, qkv=qkv)
+            gu, h = fused.linear_rms_norm(a, xi, layer.post_attention_layernorm.weight, eps,
+                                          mlp.gate_up_proj.weight, want_h=True)
+            inp, res = fused.linear_silu(gu, mlp.down_proj.weight), h
+        logits, _ = fused.linear_rms_norm(inp, res, self.norm.weight, eps, self.lm_head.weight)
+        return logits
 
 
 def random_model(args: ModelArgs | None = None, device="cuda", dtype=torch.bfloat16,

@@ -206,6 +206,20 @@ size_t cq_prefill_workspace_size(int32_t batch, int32_t n_kv_heads, int32_t n_q_
 int cq_gemv(const void *w, const void *x, void *y, int64_t n, int32_t k, int32_t dtype,
             cq_stream_t stream);
 
+/* cq_gemv of an RMSNorm'd row: h = round(x + residual) (residual null: h =
+ * x), y = W round(h * rsqrt(mean(h^2) + eps) * norm_w), the decoder's
+ * "add + RMSNorm, then project" in one launch.  h_out (optional, requires
+ * residual): h is written there.  k <= 8192; norm_w, residual, h_out
+ * 16-byte aligned. */
+int cq_gemv_rms_norm(const void *w, const void *x, const void *residual, const void *norm_w,
+                     float eps, void *h_out, void *y, int64_t n, int32_t k, int32_t dtype,
+                     cq_stream_t stream);
+
+/* cq_gemv of the SwiGLU gate of a fused [gate | up] row of 2k elements:
+ * y = W round(round(silu(gate)) * up) (cq_silu_mul's values). */
+int cq_gemv_silu(const void *w, const void *gate_up, void *y, int64_t n, int32_t k,
+                 int32_t dtype, cq_stream_t stream);
+
 /* y[r] = x[r] * rsqrt(mean(x[r]^2) + eps) * w, rows of dim elements. */
 int cq_rms_norm(const void *x, const void *w, void *y, int64_t rows, int32_t dim,
                 float eps, int32_t dtype, cq_stream_t stream);

@@ -1,5 +1,6 @@
 """GPU parity of the decoder's fused kernels (cq_rms_norm, cq_add_rms_norm,
-cq_qkv_norm_rope, cq_silu_mul, and the one-row projection cq_gemv) against torch fp32
+cq_qkv_norm_rope, cq_silu_mul, and the one-row projections cq_gemv,
+cq_gemv_rms_norm, cq_gemv_silu) against torch fp32
 statements of the same math, rounded once to the tensor dtype, plus closed
 forms: a constant row normalises to the weight, position 0 is the identity
 rotation, a rotation keeps each pair's norm, out-of-range positions give NaN.
@@ -177,6 +178,51 @@ def test_gemv(dtype, n, k):
     tol = ULP[dtype] * ref.float().abs() + k * 2.0 ** -23 * mag + TINY[dtype]
     assert (err <= tol).all(), (err - tol).max().item()
     assert got.shape == (1, 1, n) and got.dtype == dtype
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("n,k,with_res", [(6144, 4096, False), (24576, 4096, True), (13, 72, True),
+                                          (100, 8192, True)])
+def test_gemv_rms_norm(dtype, n, k, with_res):
+    # One launch of "h = x + residual; y = W rms_norm(h)" against the unfused
+    # library ops (cq_add_rms_norm / cq_rms_norm, then cq_gemv): h bit-exact;
+    # y equal except where the two kernels' fp32 sums of squares round the
+    # inverse norm to neighbouring values (a rare 1-ulp change of a normed
+    # element, which moves y by at most |w| ulp(x) over k terms).
+    from chronoquant_mlx_amd.models import fused
+    g = torch.Generator(device="cuda").manual_seed(n + 3 * k)
+    w = (torch.randn(n, k, device="cuda", generator=g) * 0.02).to(dtype)
+    x = torch.randn(1, 1, k, device="cuda", generator=g).to(dtype)
+    res = torch.randn(1, 1, k, device="cuda", generator=g).to(dtype) if with_res else None
+    nw = (1 + 0.1 * torch.randn(k, device="cuda", generator=g)).to(dtype)
+    y, h = fused.linear_rms_norm(x, res, nw, 1e-6, w, want_h=with_res)
+    if with_res:
+        h_ref, xn = fused.add_rms_norm(x, res, nw, 1e-6)
+        assert torch.equal(h.view(torch.int16), h_ref.view(torch.int16))
+    else:
+        assert h is None
+        xn = fused.rms_norm(x, nw, 1e-6)
+    ref = fused.linear(xn, w)
+    mag = (xn.float().abs().reshape(1, k) @ w.float().abs().t()).reshape(1, 1, n)
+    tol = 2 * ULP[dtype] * ref.float().abs() + ULP[dtype] * mag + TINY[dtype]
+    assert ((y.float() - ref.float()).abs() <= tol).all()
+    same = (y.view(torch.int16) == ref.view(torch.int16)).float().mean().item()
+    assert same >= 0.95, same
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("n,k", [(4096, 12288), (17, 64)])
+def test_gemv_silu(dtype, n, k):
+    # One launch of "y = W silu_mul(gate | up)" against cq_silu_mul then
+    # cq_gemv: the gate values are the same rounded numbers, so y agrees
+    # bit for bit.
+    from chronoquant_mlx_amd.models import fused
+    g = torch.Generator(device="cuda").manual_seed(n + k)
+    w = (torch.randn(n, k, device="cuda", generator=g) * 0.02).to(dtype)
+    gu = (torch.randn(1, 1, 2 * k, device="cuda", generator=g) * 2).to(dtype)
+    y = fused.linear_silu(gu, w)
+    ref = fused.linear(fused.silu_mul(gu), w)
+    assert torch.equal(y.view(torch.int16), ref.view(torch.int16))
 
 
 def test_argument_errors():
