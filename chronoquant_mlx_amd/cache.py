@@ -109,6 +109,7 @@ class ChronoQuantCache:
         self._max_len = 0
         self._dev_pos = None  # device positions (bind_device_position)
         self._dev_len = None
+        self._len_owner = True  # this cache computes _dev_len = pos + S
 
     # ------------------------------------------------------------------
     # counting (cache.py:53-61)
@@ -265,7 +266,8 @@ class ChronoQuantCache:
             _lib.call("cq_append", self._descriptor(), keys.data_ptr(), ks, values.data_ptr(), vs,
                       _lib.dtype_code(keys.dtype), S, self._dev_pos.data_ptr(), 0,
                       _lib.stream_of(keys))
-            torch.add(self._dev_pos, S, out=self._dev_len)
+            if self._len_owner:
+                torch.add(self._dev_pos, S, out=self._dev_len)
             return keys, values
         self._ensure_capacity(self.offset + S)
         _lib.call("cq_append", self._descriptor(), keys.data_ptr(), ks, values.data_ptr(), vs,
@@ -277,7 +279,9 @@ class ChronoQuantCache:
     # ------------------------------------------------------------------
     # device positions (graph-captured serving loops; no reference counterpart)
     # ------------------------------------------------------------------
-    def bind_device_position(self, pos: torch.Tensor | None, max_len: int = 0):
+    def bind_device_position(self, pos: torch.Tensor | None, max_len: int = 0,
+                             lengths: torch.Tensor | None = None,
+                             update_lengths: bool = True):
         """Take positions from device memory instead of the host offset.
 
         With `pos` (int32 [B], on the cache's device) bound, update_and_fetch
@@ -288,16 +292,26 @@ class ChronoQuantCache:
         advance() after each step.  Room for max_len tokens is reserved now
         (no reallocation may happen under capture).  pos=None returns to host
         offsets.
+
+        Caches stepped together (the layers of one model) can share the
+        per-sequence length vector pos + S: pass the same `lengths` tensor
+        to each and let one of them (update_lengths=True, appended first in
+        every step) compute it.
         """
         if pos is None:
             self._dev_pos = self._dev_len = None
+            self._len_owner = True
             self._max_len = self.offset
             return
         if pos.dtype != torch.int32 or pos.dim() != 1:
             raise TypeError("pos must be an int32 vector [B]")
+        if lengths is not None and (lengths.shape != pos.shape or lengths.dtype != pos.dtype
+                                    or lengths.device != pos.device):
+            raise TypeError("lengths must match pos (int32 [B], same device)")
         self.reserve(max_len)
         self._dev_pos = pos
-        self._dev_len = torch.empty_like(pos)
+        self._dev_len = torch.empty_like(pos) if lengths is None else lengths
+        self._len_owner = lengths is None or bool(update_lengths)
         self._max_len = int(max_len)
 
     def advance(self, n: int):

@@ -251,8 +251,10 @@ class GraphDecoder:
         self.model, self.caches = model, caches
         self.pos = torch.tensor([caches[0].offset] * batch, dtype=torch.int32, device=dev)
         self.tok = torch.zeros(batch, 1, dtype=torch.long, device=dev)
-        for c in caches:
-            c.bind_device_position(self.pos, max_len)
+        # one length vector pos + 1 for all layers, computed by the first
+        lens = torch.empty_like(self.pos)
+        for i, c in enumerate(caches):
+            c.bind_device_position(self.pos, max_len, lengths=lens, update_lengths=i == 0)
         self.graph = None
 
     def _step(self):
