@@ -10,14 +10,14 @@
 // the online (flash) form, with the weights rounded to fp16 where they enter
 // the P.V product.
 //
-// Workgroup = 8 waves = 128 query rows of one kv head: 128 / G positions x the
+// Workgroup = 16 waves = 256 query rows of one kv head: 256 / G positions x the
 // G q heads of the group (row R: position p0 + R / G, head R % G), over one
 // of nsplit contiguous pieces of its key range (split-K: without splits a
 // chunk's grid is about one workgroup per CU, which leaves every load's
-// latency exposed; splits give each CU several).  128 rows share each
-// rebuilt block, so the rebuild costs half of what it would for 64.  Per
-// 64-key block:
-//   1. waves 0-3 rebuild the K block (row-major), waves 4-7 the V block
+// latency exposed; splits give each CU several).  256 rows share each
+// rebuilt block, so the rebuild costs a quarter of what it would for 64.
+// Per 64-key block:
+//   1. waves 0-7 rebuild the K block (row-major), waves 8-15 the V block
 //      (transposed, dims x keys) in LDS with the reference's fp16 rounding;
 //   2. each wave computes S^T = K . Q^T for its 16 rows (v_mfma_f32_16x16x32_f16,
 //      4 key tiles x 4 K-steps), so a lane holds 16 scores of one row;
@@ -47,9 +47,9 @@ typedef float f4_t __attribute__((ext_vector_type(4)));
 typedef int i4_t __attribute__((ext_vector_type(4)));
 
 constexpr int kD = 128;
-constexpr int kRows = 128;       // query rows per workgroup
+constexpr int kRows = 256;       // query rows per workgroup
 constexpr int kKeys = 64;        // keys per block
-constexpr int kThreads = 512;    // 8 waves: 16 rows each
+constexpr int kThreads = 1024;   // 16 waves: 16 rows each
 constexpr int kKStride = kD + 8;      // K block row stride (fp16 elements)
 constexpr int kVStride = kKeys + 8;   // V^T block row stride (fp16 elements)
 constexpr float kTau = 8.f;
@@ -98,6 +98,10 @@ __device__ __forceinline__ f4_t mfma32(h8_t a, h8_t b, f4_t c) {
 __device__ __forceinline__ uint4 bload128(__amdgpu_buffer_rsrc_t r, uint32_t off) {
   const i4_t v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0);
   return uint4{(uint32_t)v[0], (uint32_t)v[1], (uint32_t)v[2], (uint32_t)v[3]};
+}
+__device__ __forceinline__ uint2 bload64(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  const __attribute__((ext_vector_type(2))) int v = __builtin_amdgcn_raw_buffer_load_b64(r, (int)off, 0, 0);
+  return uint2{(uint32_t)v[0], (uint32_t)v[1]};
 }
 __device__ __forceinline__ uint32_t bload32(__amdgpu_buffer_rsrc_t r, uint32_t off) {
   return (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(r, (int)off, 0, 0);
@@ -240,11 +244,11 @@ __device__ __forceinline__ void split_epilogue(const PrefillArgs &a, int b, int 
 // Bf16: queries (and output) are bf16.  The reference then computes the
 // scores in fp32 (bf16 x fp16 promotes), so they are not rounded to fp16.
 // Pow2: both strides are powers of two (token -> anchor / slot by shifts).
-// At most 128 VGPRs (4 waves per SIMD, two workgroups per CU): the waiting
-// workgroup's block loads overlap the other's products.  Keeping the next
-// block's raw data in registers instead (a software prefetch) needs ~160
-// VGPRs, one workgroup per CU, and measured slower (188 vs 167 us on the c4
-// chunk).
+// At most 128 VGPRs (4 waves per SIMD): the waves waiting on their block's
+// loads overlap the others' products.  Keeping the next block's raw data in
+// registers instead (a software prefetch) needs ~160 VGPRs and fewer waves,
+// and measured slower (188 vs 167 us on the c4 chunk at 128 rows per
+// workgroup).
 template <bool Bf16, bool Pow2>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4, 4)))
 void prefill_mfma_kernel(PrefillArgs a) {
@@ -308,19 +312,19 @@ void prefill_mfma_kernel(PrefillArgs a) {
   // this split's blocks [kb_lo, kb_hi) of the tile's n_all (possibly none)
   const int kb_lo = split * n_all / a.nsplit, kb_hi = (split + 1) * n_all / a.nsplit;
 
-  // Block staging: waves 0-3 load and rebuild the K block, waves 4-7 the V
+  // Block staging: waves 0-7 load and rebuild the K block, waves 8-15 the V
   // block, so that each thread holds one component's raw data in registers.
-  //   K (thread st = tid): key (st % 16) + 16 (st / 64), dims 32 ((st / 16) % 4)
-  //   .. +31 (4 code words): the lanes of one 16-byte LDS write phase are
-  //   consecutive keys of one quarter row (rows 68 dwords apart), which keeps
-  //   the writes conflict-free for 32- and 64-bank LDS alike.
-  //   V (thread st = tid - 256): code word st / 16 (dims 8w .. 8w+7), keys
-  //   4 (st % 16) .. +3.  The lanes of a 64-bit LDS write then cover keys
-  //   0..63 of V^T rows 8 apart (8 * 36 dwords = 32 banks): conflict-free.
-  //   (With the roles swapped, lanes 8 rows apart hit 8 banks: an 8-way
-  //   conflict on every V^T write.)  V^T rows 8..15 of every 16 hold their
-  //   4-key groups swapped in pairs (vt_col), so that the P.V reads of rows r
-  //   and r + 8, which share banks at 32 banks, touch different ones.
+  //   K (thread st = tid): key (st % 16) + 16 (st / 128), dims 16 ((st / 16)
+  //   % 8) .. +15 (2 code words): the lanes of one 16-byte LDS write phase
+  //   are consecutive keys (rows 68 dwords apart), which keeps the writes
+  //   conflict-free for 32- and 64-bank LDS alike.
+  //   V (thread st = tid - 512): code word st / 32 (dims 8w .. 8w+7), keys
+  //   2 (st % 32), +1.  The lanes of a 32-bit LDS write then cover keys
+  //   0..63 of one V^T row, and the two rows of a 64-lane phase are 8 apart
+  //   (8 * 36 dwords = 32 banks): conflict-free.  V^T rows 8..15 of every 16
+  //   hold their 4-key groups swapped in pairs (vt_col), so that the P.V
+  //   reads of rows r and r + 8, which share banks at 32 banks, touch
+  //   different ones.
   const bool kside = tid < kThreads / 2;  // wave-uniform
   const int st = tid & (kThreads / 2 - 1);
   const int c = kside ? 0 : 1;
@@ -330,12 +334,12 @@ void prefill_mfma_kernel(PrefillArgs a) {
   const __amdgpu_buffer_rsrc_t r_kf = make_rsrc(a.kf[c] + bh * a.cap_kf[c] * kD, (uint32_t)(a.cap_kf[c] * kD * 2));
   const __amdgpu_buffer_rsrc_t r_pk = make_rsrc(a.pk[c] + bh * a.cap_pf[c] * 16, (uint32_t)(a.cap_pf[c] * 64));
   const __amdgpu_buffer_rsrc_t r_sc = make_rsrc(a.sc[c] + bh * a.cap_pf[c], (uint32_t)(a.cap_pf[c] * 2));
-  const int kkey = (st & 15) | ((st >> 6) << 4), kqd = (st >> 4) & 3;
-  const int vw = st >> 4, vkq = st & 15;
+  const int kkey = (st & 15) | ((st >> 7) << 4), ke = (st >> 4) & 7;
+  const int vw = st >> 5, vkp = st & 31;
   uint32_t magic;  // fp16 1024 in both halves, an opaque VGPR for the byte permutes
   asm volatile("v_mov_b32 %0, 0x64006400" : "=v"(magic));
-  uint32_t r_cw[4], r_s[4];  // K: code words of the quarter row, scale in r_s[0]
-  uint4 r_an[4];             //    anchor dims 32 kqd + 8j ..; V: per key j
+  uint32_t r_cw[2], r_s[2];  // K: code words 2ke, 2ke + 1, scale in r_s[0]; V: per key j
+  uint4 r_an[2];             // K: anchor dims 16 ke + 8j ..; V: per key j, dims 8vw ..
   // token t -> anchor index g (-1 past the end) and P-frame slot (-1:
   // I-frame or past the end)
   auto locate = [&](int t, int &g, int &slot) {
@@ -355,18 +359,16 @@ void prefill_mfma_kernel(PrefillArgs a) {
       locate(k0 + kkey, g, slot);
       const uint32_t arow = g >= 0 ? (uint32_t)g * 256u : 0x80000000u;
       r_s[0] = bload16(r_sc, (uint32_t)slot * 2u);
-      const uint4 cw = bload128(r_pk, (uint32_t)slot * 64u + 16u * kqd);
+      const uint2 cw = bload64(r_pk, (uint32_t)slot * 64u + 8u * ke);
       r_cw[0] = cw.x;
       r_cw[1] = cw.y;
-      r_cw[2] = cw.z;
-      r_cw[3] = cw.w;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) r_an[j] = bload128(r_kf, arow + 64u * kqd + 16u * j);
+      for (int j = 0; j < 2; ++j) r_an[j] = bload128(r_kf, arow + 32u * ke + 16u * j);
     } else {
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
+      for (int j = 0; j < 2; ++j) {
         int g, slot;
-        locate(k0 + 4 * vkq + j, g, slot);
+        locate(k0 + 2 * vkp + j, g, slot);
         const uint32_t arow = g >= 0 ? (uint32_t)g * 256u : 0x80000000u;
         r_s[j] = bload16(r_sc, (uint32_t)slot * 2u);
         r_cw[j] = bload32(r_pk, (uint32_t)slot * 64u + 4u * vw);
@@ -378,27 +380,26 @@ void prefill_mfma_kernel(PrefillArgs a) {
   for (int kb = kb_lo; kb < kb_hi; ++kb) {
     const int k0 = kb * kKeys;
     load_block(k0);
-    // ---- 1. rebuild the K (waves 0-3) or V (waves 4-7) block in LDS ------------
+    // ---- 1. rebuild the K (waves 0-7) or V (waves 8-15) block in LDS -----------
     if (kside) {
       const h2_t s2 = as_h2(r_s[0] * 0x10001u);
-      uint4 *dst = (uint4 *)&lds.k[kkey][32 * kqd];
+      uint4 *dst = (uint4 *)&lds.k[kkey][16 * ke];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) dst[j] = rebuild8(r_cw[j], r_an[j], s2, magic);
+      for (int j = 0; j < 2; ++j) dst[j] = rebuild8(r_cw[j], r_an[j], s2, magic);
     } else {
-      uint4 r[4];
+      uint4 r[2];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) r[j] = rebuild8(r_cw[j], r_an[j], as_h2(r_s[j] * 0x10001u), magic);
-      // transpose: row 8w + i of V^T holds grouped-order dim i of the 4 keys
+      for (int j = 0; j < 2; ++j) r[j] = rebuild8(r_cw[j], r_an[j], as_h2(r_s[j] * 0x10001u), magic);
+      // transpose: row 8w + i of V^T holds grouped-order dim i of the 2 keys
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
         const int dw = i >> 1;
         const uint32_t sel = (i & 1) ? 0x07060302u : 0x05040100u;
         const uint32_t w0 = dw == 0 ? r[0].x : dw == 1 ? r[0].y : dw == 2 ? r[0].z : r[0].w;
         const uint32_t w1 = dw == 0 ? r[1].x : dw == 1 ? r[1].y : dw == 2 ? r[1].z : r[1].w;
-        const uint32_t w2 = dw == 0 ? r[2].x : dw == 1 ? r[2].y : dw == 2 ? r[2].z : r[2].w;
-        const uint32_t w3 = dw == 0 ? r[3].x : dw == 1 ? r[3].y : dw == 2 ? r[3].z : r[3].w;
-        *(uint2 *)&lds.v[8 * vw + i][vt_col(8 * vw + i, vkq)] =
-            uint2{__builtin_amdgcn_perm(w1, w0, sel), __builtin_amdgcn_perm(w3, w2, sel)};
+        const int row = 8 * vw + i;
+        *(uint32_t *)&lds.v[row][vt_col(row, vkp >> 1) + 2 * (vkp & 1)] =
+            __builtin_amdgcn_perm(w1, w0, sel);
       }
     }
     __syncthreads();

@@ -117,4 +117,4 @@ def prefill_supported(queries: torch.Tensor, cache, mask) -> bool:
     return (L > 1 and D == 128 and queries.dtype in (torch.float16, torch.bfloat16)
             and (mask is None or (isinstance(mask, str) and mask == "causal"))
             and cache.offset >= L and nq % cache._shape[1] == 0
-            and 128 % (nq // cache._shape[1]) == 0)
+            and 256 % (nq // cache._shape[1]) == 0)

@@ -171,7 +171,7 @@ int cq_fp16_decode_attn(const uint16_t *k, const uint16_t *v,
  * mask None or "causal" (reference attention.py:61-74 over cache.py:131-160):
  * K/V rebuilt as fp16(anchor + fp16(fp16(code) * scale)), q' = fp16(q *
  * fp16(scale)), fp16 scores, fp32 softmax, fp16 weights, fp16 output.
- * head_dim 128, n_q_heads / n_kv_heads dividing 128.  q_dtype CQ_F16 or
+ * head_dim 128, n_q_heads / n_kv_heads dividing 256.  q_dtype CQ_F16 or
  * CQ_BF16 (bf16: q' = bf16(q * bf16(scale)) and fp32 scores, as the
  * reference's bf16 x fp16 promotion computes them; output bf16).
  * q, out: [B][n_q_heads][n_q][128] of q_dtype, 16-byte aligned.
