@@ -163,39 +163,62 @@ struct AppendArgs {
   const void *x[2];
   int64_t xs[2][3];  // element strides b, h, s
   int B, H, D, W;
-  int64_t S;
+  int S;             // new tokens per sequence (2 B S H rows < 2^31, host-checked)
+  int vec;           // 16-bit dtype, E = 2, unit element stride, even row starts:
+                     // each lane's 2 elements are one aligned 32-bit load
   const int32_t *offsets;
   int64_t offset;
 };
 
+// n / d for 0 <= n < 2^31, d >= 1: a float estimate, then the remainder
+// brought into [0, d) (the estimate is off by at most one below 2^24 and by
+// a few units up to 2^31, so the loops run at most a handful of times).
+__device__ __forceinline__ int div_pos(int n, int d) {
+  int q = (int)((float)n / (float)d);
+  int r = n - q * d;
+  while (r < 0) { --q; r += d; }
+  while (r >= d) { ++q; r -= d; }
+  return q;
+}
+
 template <int DT>
 __global__ __launch_bounds__(256) void append_kernel(AppendArgs a) {
   const int lane = threadIdx.x & 63;
-  int64_t item = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
-  const int64_t per_comp = (int64_t)a.B * a.S * a.H;
+  // 32-bit index arithmetic (the host bounds 2 B S H); the row decomposition
+  // and t / stride are the only divisions, each a float estimate + fix-up
+  int item = (int)blockIdx.x * (int)(blockDim.x >> 6) + (int)(threadIdx.x >> 6);
+  const int per_comp = a.B * a.S * a.H;
   if (item >= 2 * per_comp) return;  // wave-uniform
-  const int ci = (int)(item / per_comp);
+  const int ci = item >= per_comp ? 1 : 0;
   item -= ci * per_comp;
-  const int h = (int)(item % a.H);
-  item /= a.H;
-  const int64_t s = item % a.S;
-  const int b = (int)(item / a.S);
+  const int bs = div_pos(item, a.H);
+  const int h = item - bs * a.H;
+  const int b = div_pos(bs, a.S);
+  const int s = bs - b * a.S;
 
   const cq_component &c = a.comp[ci];
   const int D = a.D, W = a.W, E = dims_per_lane(D);
   const int64_t off = a.offsets ? (int64_t)a.offsets[b] : a.offset;
   const int64_t t = off + s;
   const int stride = c.stride;
-  const int64_t g = t / stride;
+  const int64_t g = (t < 0x7fffffff) ? (int64_t)div_pos((int)t, stride) : t / stride;
   const int64_t bh = (int64_t)b * a.H + h;
   const void *x = a.x[ci];
-  const int64_t xrow = b * a.xs[ci][0] + h * a.xs[ci][1] + s * a.xs[ci][2];
+  const int64_t xrow = b * a.xs[ci][0] + h * a.xs[ci][1] + (int64_t)s * a.xs[ci][2];
 
   float v[kMaxE];
+  if (a.vec) {  // one 32-bit load of this lane's 2 elements
+    const uint32_t u = ((const uint32_t *)x)[(xrow >> 1) + lane];
+    v[0] = DT == CQ_BF16 ? bf2f((uint16_t)(u & 0xffffu)) : h2f((uint16_t)(u & 0xffffu));
+    v[1] = DT == CQ_BF16 ? bf2f((uint16_t)(u >> 16)) : h2f((uint16_t)(u >> 16));
 #pragma unroll
-  for (int i = 0; i < kMaxE; ++i) {
-    const int dim = lane * E + i;
-    v[i] = (i < E && dim < D) ? Dt<DT>::load(x, xrow + dim) : 0.f;
+    for (int i = 2; i < kMaxE; ++i) v[i] = 0.f;
+  } else {
+#pragma unroll
+    for (int i = 0; i < kMaxE; ++i) {
+      const int dim = lane * E + i;
+      v[i] = (i < E && dim < D) ? Dt<DT>::load(x, xrow + dim) : 0.f;
+    }
   }
 
   if (t - g * stride == 0) {  // I-frame: fp16(token), reference cache.py:103-105
@@ -226,11 +249,19 @@ __global__ __launch_bounds__(256) void append_kernel(AppendArgs a) {
     }
   } else {
     const uint16_t *arow = c.keyframes + (bh * c.cap_keyframes + g) * D;
+    if (a.vec) {  // D = 2 * 64 here: the anchor row's 2 elements, one load
+      const uint32_t u = ((const uint32_t *)arow)[lane];
+      d[0] = Dt<DT>::round(v[0] - Dt<DT>::round(h2f((uint16_t)(u & 0xffffu))));
+      d[1] = Dt<DT>::round(v[1] - Dt<DT>::round(h2f((uint16_t)(u >> 16))));
 #pragma unroll
-    for (int i = 0; i < kMaxE; ++i) {
-      const int dim = lane * E + i;
-      const float an = (i < E && dim < D) ? h2f(arow[dim]) : 0.f;
-      d[i] = Dt<DT>::round(v[i] - Dt<DT>::round(an));
+      for (int i = 2; i < kMaxE; ++i) d[i] = 0.f;
+    } else {
+#pragma unroll
+      for (int i = 0; i < kMaxE; ++i) {
+        const int dim = lane * E + i;
+        const float an = (i < E && dim < D) ? h2f(arow[dim]) : 0.f;
+        d[i] = Dt<DT>::round(v[i] - Dt<DT>::round(an));
+      }
     }
   }
   int code[kMaxE];
@@ -393,10 +424,18 @@ int cq_append(const cq_cache_desc *cache, const void *keys, const int64_t *key_s
   a.H = cache->n_kv_heads;
   a.D = cache->head_dim;
   a.W = (cache->head_dim + 7) / 8;
-  a.S = n_new;
+  const int64_t items = 2 * (int64_t)a.B * n_new * a.H;
+  if (items >= 0x7fffffff - 4) return CQ_ERR_SHAPE;  // 32-bit row indices in the kernel
+  a.S = (int)n_new;
+  // 16-bit dtype, D = 128 (2 elements per lane), unit element stride, even
+  // row strides and 4-byte aligned bases: each lane loads its 2 elements at once
+  a.vec = (dtype == CQ_F16 || dtype == CQ_BF16) && a.D == 128 &&
+          key_strides[2] >= 0 && value_strides[2] >= 0 &&
+          ((key_strides[0] | key_strides[1] | key_strides[2] | value_strides[0] |
+            value_strides[1] | value_strides[2]) & 1) == 0 &&
+          (((uintptr_t)keys | (uintptr_t)values) & 3) == 0;
   a.offsets = offsets;
   a.offset = offset;
-  const int64_t items = 2 * (int64_t)a.B * a.S * a.H;
   const dim3 grid((unsigned)((items + 3) / 4)), block(256);
   hipStream_t s = (hipStream_t)stream;
   switch (dtype) {
