@@ -315,7 +315,8 @@ size_t cq_decode_workspace_size(int32_t batch, int32_t n_kv_heads, int32_t n_q_h
                                 int32_t head_dim, int64_t max_seq_len) {
   if (batch < 1 || n_kv_heads < 1 || n_q_heads < 1 || head_dim < 1) return 0;
   // enough for the grid plan of every decode kernel and for the balanced
-  // plan of the GQA-4 kernel
+  // plan of the MFMA kernels (at most resident / n_kv_heads workgroups per
+  // column)
   const SplitPlan p = plan_splits((int64_t)batch * n_kv_heads, max_seq_len, decode_max_resident());
   const int64_t bal = balanced_slots(std::max((int64_t)1, decode_max_resident() / n_kv_heads),
                                      max_seq_len);

@@ -157,22 +157,27 @@ def test_ragged_lengths(generic, lens):
                          mfma=not generic)
 
 
-@pytest.mark.parametrize("B,H,T,seed", [(40, 8, 3000, 41), (1030, 1, 96, 42)])
-def test_balanced_plan_many_sequences(B, H, T, seed):
-    # The GQA-4 kernel lays the batch's 512-token units end to end and gives
-    # every workgroup of a kv head the same share, so a workgroup's range
-    # ends one sequence and starts the next, and a sequence's pieces combine
-    # across workgroups.  B=40 uses the per-sequence unit table (lengths
-    # 0..3000); B=1030 is past the table's 1024 sequences and takes the
-    # uniform unit space, where each workgroup covers several sequences.
+@pytest.mark.parametrize("B,H,T,G,sk,sv,seed", [
+    (40, 8, 3000, 4, 32, 8, 41), (1030, 1, 96, 4, 32, 8, 42),
+    (40, 2, 3000, 8, 32, 8, 44), (24, 2, 2600, 20, 12, 20, 45), (1030, 1, 96, 8, 16, 4, 46)])
+def test_balanced_plan_many_sequences(B, H, T, G, sk, sv, seed):
+    # The MFMA kernels lay the batch's 512-token units end to end and give
+    # every workgroup of a (kv head, q-head chunk) column the same share, so
+    # a workgroup's range ends one sequence and starts the next, and a
+    # sequence's pieces combine across workgroups.  B=40 / 24 use the
+    # per-sequence unit table (lengths 0..T); B=1030 is past the table's 1024
+    # sequences and takes the uniform unit space, where each workgroup covers
+    # several sequences.  G=4 with power-of-two strides runs the GQA-4
+    # kernel; G=8 and G=20 (two q-head chunks, strides 12 / 20 on the
+    # float-reciprocal path) the 16-head kernel.
     rng = np.random.default_rng(seed)
-    D, G = 128, 4
+    D = 128
     k = np.cumsum(rng.standard_normal((B, H, T, D)) * 0.1, axis=2).astype(np.float16)
     v = np.cumsum(rng.standard_normal((B, H, T, D)) * 0.1, axis=2).astype(np.float16)
     q = rng.standard_normal((B, G * H, D)).astype(np.float16)
     lens = rng.integers(0, T + 1, size=B)
     lens[:3] = [0, T, 1]
-    params = dict(stride_k=32, stride_v=8)
+    params = dict(stride_k=sk, stride_v=sv)
     cache = build_gpu_cache(k, v, **params)
     scale = D ** -0.5
     for _ in range(2):
@@ -187,11 +192,12 @@ def test_balanced_plan_many_sequences(B, H, T, seed):
                 assert_close(out[b], oracle_fallback(ck, cv, q[b], scale), what=f"b={b} L={L}")
 
 
-def test_uniform_batch_ranges_across_sequences():
-    # 3 sequences of 16384 tokens over 32 workgroups per kv head: 3 units per
+@pytest.mark.parametrize("G", [4, 8])
+def test_uniform_batch_ranges_across_sequences(G):
+    # 3 sequences of 16384 tokens over 32 workgroups per column: 3 units per
     # workgroup, so some workgroups end one sequence and start the next.
     rng = np.random.default_rng(43)
-    B, H, T, D, G = 3, 8, 16384, 128, 4
+    B, H, T, D = 3, 8, 16384, 128
     k = np.cumsum(rng.standard_normal((B, H, T, D)) * 0.05, axis=2).astype(np.float16)
     v = np.cumsum(rng.standard_normal((B, H, T, D)) * 0.05, axis=2).astype(np.float16)
     q = rng.standard_normal((B, G * H, D)).astype(np.float16)
