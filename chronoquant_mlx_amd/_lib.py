@@ -83,6 +83,8 @@ SIGNATURES = {
     "cq_add_rms_norm": ([_P, _P, _P, _P, _P, _I64, _I32, _F, _I32, _P], _I32),
     "cq_qkv_norm_rope": ([_P, _P, _P, _P, _P, _P, _P, _P, _I64, _P, _I64, _I32, _I64, _I32, _I32,
                           _I32, _F, _I32, _P], _I32),
+    "cq_qkv_rope_append": ([_DESC, _P, _P, _P, _P, _P, _P, _I64, _P, _I64, _I32, _F, _I32, _P,
+                            _I64, _P, _P], _I32),
     "cq_silu_mul": ([_P, _P, _I64, _I64, _I32, _P], _I32),
     "cq_status_string": ([_I32], ctypes.c_char_p),
 }

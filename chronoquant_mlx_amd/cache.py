@@ -276,6 +276,54 @@ class ChronoQuantCache:
         self._max_len = self.offset
         return keys, values
 
+    def fused_decode_append(self, qkv: torch.Tensor, n_q_heads: int,
+                            q_weight: torch.Tensor | None, k_weight: torch.Tensor | None,
+                            cos: torch.Tensor, sin: torch.Tensor, positions: torch.Tensor,
+                            eps: float) -> torch.Tensor | None:
+        """One new token per sequence straight from a fused QKV projection
+        qkv [B, 1, (n_q_heads + 2 H) * 128]: RMSNorm and rotary embedding of
+        the query and key heads, and the append of the key and value heads,
+        in one launch (cq_qkv_rope_append).  The same bits as
+        fused.qkv_norm_rope followed by update_and_fetch (cache.py:198-215 in
+        the reference; no counterpart for the fusion).  Returns q [B,
+        n_q_heads, 1, 128], or None when the cache cannot take the token this
+        way (not shaped by an earlier append, another head_dim, batch or head
+        count): the caller then runs the two steps."""
+        if self._shape is None:
+            return None
+        B, H, D = self._shape
+        if D != 128 or qkv.shape != (B, 1, (n_q_heads + 2 * H) * D) or qkv.device != self._device:
+            return None
+        for t in (cos, sin):
+            if t.dtype != torch.float32 or t.dim() != 2 or t.shape[1] != D // 2 or t.device != qkv.device:
+                raise ValueError("fused_decode_append: cos/sin must be fp32 [max_pos, 64] on qkv's device")
+        for w in (q_weight, k_weight):
+            if w is not None and (w.shape != (D,) or w.dtype != qkv.dtype or w.device != qkv.device):
+                raise ValueError("fused_decode_append: norm weights must be [128] of qkv's dtype")
+        positions = positions.to(device=qkv.device, dtype=torch.int64)
+        if positions.numel() == 1:
+            bstride = 0
+        elif positions.shape in ((B,), (B, 1)):
+            bstride = 1
+        else:
+            raise ValueError("fused_decode_append: positions must be [1], [B] or [B, 1]")
+        qkv, cos, sin, positions = qkv.contiguous(), cos.contiguous(), sin.contiguous(), positions.contiguous()
+        q = torch.empty(B, n_q_heads, 1, D, dtype=qkv.dtype, device=qkv.device)
+        if self._dev_pos is not None:
+            offsets, offset = self._dev_pos.data_ptr(), 0
+            lengths = self._dev_len.data_ptr() if self._len_owner else None
+        else:
+            self._ensure_capacity(self.offset + 1)
+            offsets, offset, lengths = None, self.offset, None
+        _lib.call("cq_qkv_rope_append", self._descriptor(), qkv.data_ptr(), _lib.ptr(q_weight),
+                  _lib.ptr(k_weight), q.data_ptr(), cos.data_ptr(), sin.data_ptr(), cos.shape[0],
+                  positions.data_ptr(), bstride, n_q_heads, float(eps),
+                  _lib.dtype_code(qkv.dtype), offsets, offset, lengths, _lib.stream_of(qkv))
+        if self._dev_pos is None:
+            self.offset += 1
+            self._max_len = self.offset
+        return q
+
     # ------------------------------------------------------------------
     # device positions (graph-captured serving loops; no reference counterpart)
     # ------------------------------------------------------------------

@@ -181,6 +181,64 @@ __device__ __forceinline__ int div_pos(int n, int d) {
   return q;
 }
 
+// Encode one token (this lane's E dims in v) at position t of row bh of
+// component c, g = t / stride: the fp16 I-frame when t is a multiple of the
+// stride (reference cache.py:103-105), else the residual against anchor g
+// (cache.py:107-116), quantised and packed into P-frame slot t - g - 1.
+// an_given: the anchor's dims are in an (an I-frame appended by the same
+// call, not in the cache yet); otherwise the cache's anchor row is read.
+// vec: D = 128, so the lane's 2 anchor elements are one 32-bit load.
+// Rows past the capacities, and negative positions, are dropped (device
+// positions: the host could not check them).
+template <int DT>
+__device__ __forceinline__ void encode_token(const cq_component &c, int64_t bh, int64_t t,
+                                             int64_t g, const float (&v)[kMaxE], bool an_given,
+                                             const float (&an)[kMaxE], int lane, int D, int W,
+                                             bool vec) {
+  const int E = dims_per_lane(D);
+  if (t < 0) return;
+  if (t - g * c.stride == 0) {
+    if (g >= c.cap_keyframes) return;
+    uint16_t *row = c.keyframes + (bh * c.cap_keyframes + g) * D;
+#pragma unroll
+    for (int i = 0; i < kMaxE; ++i) {
+      const int dim = lane * E + i;
+      if (i < E && dim < D) row[dim] = f2h(v[i]);
+    }
+    return;
+  }
+  const int64_t slot = t - g - 1;
+  if (slot >= c.cap_pframes || g >= c.cap_keyframes) return;
+  float d[kMaxE];
+  if (an_given) {
+#pragma unroll
+    for (int i = 0; i < kMaxE; ++i) d[i] = Dt<DT>::round(v[i] - Dt<DT>::round(an[i]));  // cache.py:113
+  } else {
+    const uint16_t *arow = c.keyframes + (bh * c.cap_keyframes + g) * D;
+    if (vec) {  // D = 2 * 64: the anchor row's 2 elements, one load
+      const uint32_t u = ((const uint32_t *)arow)[lane];
+      d[0] = Dt<DT>::round(v[0] - Dt<DT>::round(h2f((uint16_t)(u & 0xffffu))));
+      d[1] = Dt<DT>::round(v[1] - Dt<DT>::round(h2f((uint16_t)(u >> 16))));
+#pragma unroll
+      for (int i = 2; i < kMaxE; ++i) d[i] = 0.f;
+    } else {
+#pragma unroll
+      for (int i = 0; i < kMaxE; ++i) {
+        const int dim = lane * E + i;
+        const float a = (i < E && dim < D) ? h2f(arow[dim]) : 0.f;
+        d[i] = Dt<DT>::round(v[i] - Dt<DT>::round(a));
+      }
+    }
+  }
+  int code[kMaxE];
+  const float sc = codec_row<DT>(d, E, c.delta_bits, c.dead_zone, code);
+  const uint32_t word = pack_lane(code, E, lane, D);
+  const int wl = lane * E;
+  if ((wl & 7) == 0 && (wl >> 3) < W)
+    c.packed[(bh * c.cap_pframes + slot) * W + (wl >> 3)] = word;
+  if (lane == 0) c.scales[bh * c.cap_pframes + slot] = f2h(sc);
+}
+
 template <int DT>
 __global__ __launch_bounds__(256) void append_kernel(AppendArgs a) {
   const int lane = threadIdx.x & 63;
@@ -221,56 +279,99 @@ __global__ __launch_bounds__(256) void append_kernel(AppendArgs a) {
     }
   }
 
-  if (t - g * stride == 0) {  // I-frame: fp16(token), reference cache.py:103-105
-    if (g >= c.cap_keyframes) return;
-    uint16_t *row = c.keyframes + (bh * c.cap_keyframes + g) * D;
-#pragma unroll
-    for (int i = 0; i < kMaxE; ++i) {
-      const int dim = lane * E + i;
-      if (i < E && dim < D) row[dim] = f2h(v[i]);
-    }
-    return;
-  }
-
-  const int64_t slot = t - g - 1;
-  if (slot >= c.cap_pframes || g >= c.cap_keyframes) return;
   // Anchor = fp16 I-frame of group g: from the cache if it predates this
   // call, else straight from the new tokens (same fp16 value), so the waves
   // of one launch never depend on each other.
   const int64_t ta = g * stride;
-  float d[kMaxE];
-  if (ta >= off) {
+  const bool an_given = t != ta && ta >= off;
+  float an[kMaxE];
+#pragma unroll
+  for (int i = 0; i < kMaxE; ++i) an[i] = 0.f;
+  if (an_given) {
     const int64_t arow = b * a.xs[ci][0] + h * a.xs[ci][1] + (ta - off) * a.xs[ci][2];
 #pragma unroll
     for (int i = 0; i < kMaxE; ++i) {
       const int dim = lane * E + i;
-      const float an = (i < E && dim < D) ? h2f(f2h(Dt<DT>::load(x, arow + dim))) : 0.f;
-      d[i] = Dt<DT>::round(v[i] - Dt<DT>::round(an));  // cache.py:113
-    }
-  } else {
-    const uint16_t *arow = c.keyframes + (bh * c.cap_keyframes + g) * D;
-    if (a.vec) {  // D = 2 * 64 here: the anchor row's 2 elements, one load
-      const uint32_t u = ((const uint32_t *)arow)[lane];
-      d[0] = Dt<DT>::round(v[0] - Dt<DT>::round(h2f((uint16_t)(u & 0xffffu))));
-      d[1] = Dt<DT>::round(v[1] - Dt<DT>::round(h2f((uint16_t)(u >> 16))));
-#pragma unroll
-      for (int i = 2; i < kMaxE; ++i) d[i] = 0.f;
-    } else {
-#pragma unroll
-      for (int i = 0; i < kMaxE; ++i) {
-        const int dim = lane * E + i;
-        const float an = (i < E && dim < D) ? h2f(arow[dim]) : 0.f;
-        d[i] = Dt<DT>::round(v[i] - Dt<DT>::round(an));
-      }
+      an[i] = (i < E && dim < D) ? h2f(f2h(Dt<DT>::load(x, arow + dim))) : 0.f;
     }
   }
-  int code[kMaxE];
-  const float sc = codec_row<DT>(d, E, c.delta_bits, c.dead_zone, code);
-  const uint32_t word = pack_lane(code, E, lane, D);
-  const int wl = lane * E;
-  if ((wl & 7) == 0 && (wl >> 3) < W)
-    c.packed[(bh * c.cap_pframes + slot) * W + (wl >> 3)] = word;
-  if (lane == 0) c.scales[bh * c.cap_pframes + slot] = f2h(sc);
+  encode_token<DT>(c, bh, t, g, v, an_given, an, lane, D, W, a.vec != 0);
+}
+
+// ---------------------------------------------------------------------------
+// cq_qkv_rope_append: one decode token per sequence, from the fused QKV
+// projection straight into the caches.  One wavefront per (b, head) over the
+// nq query, nkv key and nkv value heads; lane j holds dims j and j + 64 (one
+// rotary pair).  Query and key heads: RMSNorm (rounded to the dtype), then
+// the rotary embedding at positions[b * pos_bstride], exactly as
+// cq_qkv_norm_rope computes them; query rows go to q_out, key rows (rounded
+// to the dtype, as that kernel's output is) and value rows are appended at
+// cache position t = offsets[b] (or offset) as cq_append encodes them.  With
+// one new token the anchor of a P-frame is always in the cache already.
+// ---------------------------------------------------------------------------
+struct RopeAppendArgs {
+  cq_component comp[2];
+  const void *qkv;  // [B][(nq + 2 nkv) * 128]
+  const void *q_w, *k_w;
+  void *q_out;                 // [B][nq][128]
+  const float *cos_t, *sin_t;  // [max_pos][64]
+  const int64_t *positions;
+  int64_t pos_bstride, max_pos;
+  const int32_t *offsets;
+  int64_t offset;
+  int32_t *lengths;  // optional: t + 1 per sequence
+  int B, nq, nkv, W;
+  float eps;
+};
+
+template <int DT>
+__global__ __launch_bounds__(256) void rope_append_kernel(RopeAppendArgs a) {
+  const int lane = threadIdx.x & 63;
+  const int heads = a.nq + 2 * a.nkv;
+  const int row = (int)blockIdx.x * 4 + (int)(threadIdx.x >> 6);
+  if (row >= a.B * heads) return;  // wave-uniform
+  const int b = div_pos(row, heads), h = row - b * heads;
+  float x1 = Dt<DT>::load(a.qkv, (int64_t)row * 128 + lane);
+  float x2 = Dt<DT>::load(a.qkv, (int64_t)row * 128 + lane + 64);
+  const int64_t t = a.offsets ? (int64_t)a.offsets[b] : a.offset;
+  if (a.lengths && h == 0 && lane == 0) a.lengths[b] = (int32_t)(t + 1);
+  if (h < a.nq + a.nkv) {
+    const bool is_q = h < a.nq;
+    const void *w = is_q ? a.q_w : a.k_w;
+    if (w) {
+      const float inv = 1.f / sqrtf(wave_sum(x1 * x1 + x2 * x2) / 128.f + a.eps);
+      x1 = Dt<DT>::round(x1 * inv * Dt<DT>::load(w, lane));
+      x2 = Dt<DT>::round(x2 * inv * Dt<DT>::load(w, lane + 64));
+    }
+    const int64_t pos = a.positions[(int64_t)b * a.pos_bstride];
+    float c = __builtin_nanf(""), s = c;
+    if (pos >= 0 && pos < a.max_pos) {
+      c = a.cos_t[pos * 64 + lane];
+      s = a.sin_t[pos * 64 + lane];
+    }
+    const float y1 = x1 * c - x2 * s, y2 = x2 * c + x1 * s;
+    if (is_q) {
+      const int64_t o = ((int64_t)b * a.nq + h) * 128;
+      Dt<DT>::store(a.q_out, o + lane, y1);
+      Dt<DT>::store(a.q_out, o + lane + 64, y2);
+      return;
+    }
+    x1 = Dt<DT>::round(y1);
+    x2 = Dt<DT>::round(y2);
+  }
+  // key or value row: to the codec's lane layout (lane holds dims 2 lane and
+  // 2 lane + 1), from lanes 2 lane mod 64 and 2 lane + 1 mod 64 of the
+  // first (lane < 32) or second half
+  const int ci = h >= a.nq + a.nkv ? 1 : 0;
+  const int hk = h - a.nq - ci * a.nkv;
+  const int s0 = (2 * lane) & 63;
+  const float a0 = __shfl(x1, s0, 64), a1 = __shfl(x1, s0 + 1, 64);
+  const float b0 = __shfl(x2, s0, 64), b1 = __shfl(x2, s0 + 1, 64);
+  float v[kMaxE] = {lane < 32 ? a0 : b0, lane < 32 ? a1 : b1, 0.f, 0.f};
+  const float none[kMaxE] = {0.f, 0.f, 0.f, 0.f};
+  const cq_component &c = a.comp[ci];
+  const int64_t g = t < 0x7fffffff ? (int64_t)div_pos((int)t, c.stride) : t / c.stride;
+  encode_token<DT>(c, (int64_t)b * a.nkv + hk, t, g, v, false, none, lane, 128, a.W, true);
 }
 
 // ---------------------------------------------------------------------------
@@ -443,6 +544,59 @@ int cq_append(const cq_cache_desc *cache, const void *keys, const int64_t *key_s
     case CQ_BF16: append_kernel<CQ_BF16><<<grid, block, 0, s>>>(a); break;
     case CQ_F32: append_kernel<CQ_F32><<<grid, block, 0, s>>>(a); break;
     default: return CQ_ERR_DTYPE;
+  }
+  return launch_status();
+}
+
+int cq_qkv_rope_append(const cq_cache_desc *cache, const void *qkv, const void *q_w,
+                       const void *k_w, void *q_out, const float *cos_t, const float *sin_t,
+                       int64_t max_pos, const int64_t *positions, int64_t pos_bstride,
+                       int32_t n_q_heads, float eps, int32_t dtype, const int32_t *offsets,
+                       int64_t offset, int32_t *lengths, cq_stream_t stream) {
+  int st = validate_cache(cache);
+  if (st) return st;
+  if (!qkv || !q_out || !cos_t || !sin_t || !positions) return CQ_ERR_ARG;
+  if (offset < 0 || max_pos < 1 || pos_bstride < 0) return CQ_ERR_ARG;
+  if (cache->head_dim != 128) return CQ_ERR_UNSUPPORTED;
+  if (n_q_heads < 1) return CQ_ERR_SHAPE;
+  if (dtype != CQ_F16 && dtype != CQ_BF16 && dtype != CQ_F32) return CQ_ERR_DTYPE;
+  if (!offsets) {
+    for (const cq_component *p : {&cache->k, &cache->v}) {
+      if (num_keyframes(offset + 1, p->stride) > p->cap_keyframes ||
+          num_pframes(offset + 1, p->stride) > p->cap_pframes)
+        return CQ_ERR_CAPACITY;
+    }
+  }
+  // the keyframe rows are read 4 bytes per lane
+  if (((uintptr_t)cache->k.keyframes | (uintptr_t)cache->v.keyframes) & 3) return CQ_ERR_ALIGN;
+  RopeAppendArgs a;
+  a.comp[0] = cache->k;
+  a.comp[1] = cache->v;
+  a.qkv = qkv;
+  a.q_w = q_w;
+  a.k_w = k_w;
+  a.q_out = q_out;
+  a.cos_t = cos_t;
+  a.sin_t = sin_t;
+  a.positions = positions;
+  a.pos_bstride = pos_bstride;
+  a.max_pos = max_pos;
+  a.offsets = offsets;
+  a.offset = offset;
+  a.lengths = lengths;
+  a.B = cache->batch;
+  a.nq = n_q_heads;
+  a.nkv = cache->n_kv_heads;
+  a.W = 16;
+  a.eps = eps;
+  const int64_t rows = (int64_t)a.B * (a.nq + 2 * a.nkv);
+  if (rows >= 0x7fffffff - 4) return CQ_ERR_SHAPE;  // 32-bit row indices in the kernel
+  const dim3 grid((unsigned)((rows + 3) / 4)), block(256);
+  hipStream_t s = (hipStream_t)stream;
+  switch (dtype) {
+    case CQ_F16: rope_append_kernel<CQ_F16><<<grid, block, 0, s>>>(a); break;
+    case CQ_BF16: rope_append_kernel<CQ_BF16><<<grid, block, 0, s>>>(a); break;
+    default: rope_append_kernel<CQ_F32><<<grid, block, 0, s>>>(a); break;
   }
   return launch_status();
 }

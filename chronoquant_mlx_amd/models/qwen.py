@@ -28,6 +28,8 @@ import torch
 import torch.nn.functional as F
 from torch import nn
 
+from .. import patch as _patch
+from ..cache import ChronoQuantCache
 from ..host import scaled_dot_product_attention  # rebound by patch.apply()
 from . import fused
 
@@ -108,13 +110,22 @@ class Attention(nn.Module):
         if qkv is None:
             qkv = fused.linear(x, self.qkv_proj.weight) if FUSED_OPS else self.qkv_proj(x)
         B, L, _ = qkv.shape
-        if FUSED_OPS:
-            q, k, v = fused.qkv_norm_rope(qkv, self.nh, self.nkv, self.q_norm.weight,
-                                          self.k_norm.weight, self.rope.cos, self.rope.sin,
-                                          positions, self.q_norm.eps)
-        else:
-            q, k, v = self._qkv_torch(qkv, positions)
-        keys, values = cache.update_and_fetch(k, v)
+        q = None
+        if FUSED_OPS and L == 1 and isinstance(cache, ChronoQuantCache) and _patch._patched:
+            # a decode token: norm, RoPE and the cache append in one launch
+            # (the patched SDPA reads the cache, not the keys / values)
+            q = cache.fused_decode_append(qkv, self.nh, self.q_norm.weight, self.k_norm.weight,
+                                          self.rope.cos, self.rope.sin, positions,
+                                          self.q_norm.eps)
+            keys = values = None
+        if q is None:
+            if FUSED_OPS:
+                q, k, v = fused.qkv_norm_rope(qkv, self.nh, self.nkv, self.q_norm.weight,
+                                              self.k_norm.weight, self.rope.cos, self.rope.sin,
+                                              positions, self.q_norm.eps)
+            else:
+                q, k, v = self._qkv_torch(qkv, positions)
+            keys, values = cache.update_and_fetch(k, v)
         out = scaled_dot_product_attention(q, keys, values, cache=cache, scale=self.scale,
                                            mask=mask)
         out = out.transpose(1, 2).reshape(B, L, self.nh * self.hd)

@@ -247,6 +247,25 @@ int cq_qkv_norm_rope(const void *qkv, const void *q_w, const void *k_w, void *q_
                      int32_t batch, int64_t seq, int32_t n_q_heads, int32_t n_kv_heads,
                      int32_t head_dim, float eps, int32_t dtype, cq_stream_t stream);
 
+/* One decode token per sequence from the fused QKV projection straight into
+ * the caches: cq_qkv_norm_rope's query and key rows, then cq_append of the
+ * key and value rows, in one launch (no counterpart in the reference, where
+ * the model's q/k norm, RoPE and cache.update_and_fetch (cache.py:198-215)
+ * are separate steps).  qkv: [batch][(n_q_heads + 2 * n_kv_heads) * 128],
+ * batch and n_kv_heads those of the cache, head_dim 128.  q_out:
+ * [batch][n_q_heads][128] of dtype.  positions as for cq_qkv_norm_rope with
+ * seq = 1 (the rotary position of sequence b at positions[b * pos_bstride]).
+ * Cache position: offsets[b] (device int32 [batch]) when non-NULL, else
+ * offset; with offsets the capacities cannot be checked on the host and
+ * rows past them are dropped.  lengths (device int32 [batch], may be NULL)
+ * receives position + 1 per sequence, the lengths the decode then reads.
+ * Bit-identical to cq_qkv_norm_rope followed by cq_append. */
+int cq_qkv_rope_append(const cq_cache_desc *cache, const void *qkv, const void *q_w,
+                       const void *k_w, void *q_out, const float *cos_t, const float *sin_t,
+                       int64_t max_pos, const int64_t *positions, int64_t pos_bstride,
+                       int32_t n_q_heads, float eps, int32_t dtype, const int32_t *offsets,
+                       int64_t offset, int32_t *lengths, cq_stream_t stream);
+
 /* y[r][c] = silu(gu[r][c]) * gu[r][n + c]: the SwiGLU gate over rows of a
  * fused [gate | up] projection (2n wide); silu rounded to dtype first. */
 int cq_silu_mul(const void *gu, void *y, int64_t rows, int64_t n, int32_t dtype,
