@@ -7,6 +7,8 @@
 #include <hip/hip_runtime.h>
 #include <math.h>
 
+#include <algorithm>
+
 #include "cq_device.h"
 
 namespace cq {
@@ -181,21 +183,52 @@ __device__ __forceinline__ int div_pos(int n, int d) {
   return q;
 }
 
-// Encode one token (this lane's E dims in v) at position t of row bh of
-// component c, g = t / stride: the fp16 I-frame when t is a multiple of the
-// stride (reference cache.py:103-105), else the residual against anchor g
-// (cache.py:107-116), quantised and packed into P-frame slot t - g - 1.
-// an_given: the anchor's dims are in an (an I-frame appended by the same
-// call, not in the cache yet); otherwise the cache's anchor row is read.
-// vec: D = 128, so the lane's 2 anchor elements are one 32-bit load.
-// Rows past the capacities, and negative positions, are dropped (device
+// The operands of one token row, held by a wave: this lane's E dims of the
+// token (v) and of its fp16 anchor (an; unused for an I-frame), and where
+// the row goes: component ci, row bh = b * H + h, position t, group g =
+// t / stride.
+struct TokenRow {
+  float v[kMaxE], an[kMaxE];
+  int64_t bh, t, g;
+  int ci;
+};
+
+// This lane's dims of keyframe row g of bh (g clamped into the capacity: a
+// token whose anchor lies past it is dropped by encode_token).  vec: D = 128,
+// the lane's 2 elements are one 32-bit load.
+__device__ __forceinline__ void load_cache_anchor(const cq_component &c, int64_t bh, int64_t g,
+                                                  int lane, int D, bool vec,
+                                                  float (&an)[kMaxE]) {
+  const int E = dims_per_lane(D);
+  const int64_t gg = g < 0 ? 0 : (g >= c.cap_keyframes ? c.cap_keyframes - 1 : g);
+  const uint16_t *arow = c.keyframes + (bh * c.cap_keyframes + gg) * D;
+  if (vec) {
+    const uint32_t u = ((const uint32_t *)arow)[lane];
+    an[0] = h2f((uint16_t)(u & 0xffffu));
+    an[1] = h2f((uint16_t)(u >> 16));
+#pragma unroll
+    for (int i = 2; i < kMaxE; ++i) an[i] = 0.f;
+  } else {
+#pragma unroll
+    for (int i = 0; i < kMaxE; ++i) {
+      const int dim = lane * E + i;
+      an[i] = (i < E && dim < D) ? h2f(arow[dim]) : 0.f;
+    }
+  }
+}
+
+// Encode one token row whose operands are loaded: the fp16 I-frame when t is
+// a multiple of the stride (reference cache.py:103-105), else the residual
+// against anchor g (cache.py:107-116: d = round(token - round(anchor))),
+// quantised and packed into P-frame slot t - g - 1.  No loads: a wave can
+// have the operands of several rows in flight before encoding any.  Rows
+// past the capacities, and negative positions, are dropped (device
 // positions: the host could not check them).
 template <int DT>
-__device__ __forceinline__ void encode_token(const cq_component &c, int64_t bh, int64_t t,
-                                             int64_t g, const float (&v)[kMaxE], bool an_given,
-                                             const float (&an)[kMaxE], int lane, int D, int W,
-                                             bool vec) {
+__device__ __forceinline__ void encode_token(const cq_component &c, const TokenRow &r, int lane,
+                                             int D, int W) {
   const int E = dims_per_lane(D);
+  const int64_t bh = r.bh, t = r.t, g = r.g;
   if (t < 0) return;
   if (t - g * c.stride == 0) {
     if (g >= c.cap_keyframes) return;
@@ -203,33 +236,15 @@ __device__ __forceinline__ void encode_token(const cq_component &c, int64_t bh, 
 #pragma unroll
     for (int i = 0; i < kMaxE; ++i) {
       const int dim = lane * E + i;
-      if (i < E && dim < D) row[dim] = f2h(v[i]);
+      if (i < E && dim < D) row[dim] = f2h(r.v[i]);
     }
     return;
   }
   const int64_t slot = t - g - 1;
   if (slot >= c.cap_pframes || g >= c.cap_keyframes) return;
   float d[kMaxE];
-  if (an_given) {
 #pragma unroll
-    for (int i = 0; i < kMaxE; ++i) d[i] = Dt<DT>::round(v[i] - Dt<DT>::round(an[i]));  // cache.py:113
-  } else {
-    const uint16_t *arow = c.keyframes + (bh * c.cap_keyframes + g) * D;
-    if (vec) {  // D = 2 * 64: the anchor row's 2 elements, one load
-      const uint32_t u = ((const uint32_t *)arow)[lane];
-      d[0] = Dt<DT>::round(v[0] - Dt<DT>::round(h2f((uint16_t)(u & 0xffffu))));
-      d[1] = Dt<DT>::round(v[1] - Dt<DT>::round(h2f((uint16_t)(u >> 16))));
-#pragma unroll
-      for (int i = 2; i < kMaxE; ++i) d[i] = 0.f;
-    } else {
-#pragma unroll
-      for (int i = 0; i < kMaxE; ++i) {
-        const int dim = lane * E + i;
-        const float a = (i < E && dim < D) ? h2f(arow[dim]) : 0.f;
-        d[i] = Dt<DT>::round(v[i] - Dt<DT>::round(a));
-      }
-    }
-  }
+  for (int i = 0; i < kMaxE; ++i) d[i] = Dt<DT>::round(r.v[i] - Dt<DT>::round(r.an[i]));
   int code[kMaxE];
   const float sc = codec_row<DT>(d, E, c.delta_bits, c.dead_zone, code);
   const uint32_t word = pack_lane(code, E, lane, D);
@@ -239,14 +254,17 @@ __device__ __forceinline__ void encode_token(const cq_component &c, int64_t bh, 
   if (lane == 0) c.scales[bh * c.cap_pframes + slot] = f2h(sc);
 }
 
+// Load phase of one (component, b, new token s, kv head) row of cq_append.
+// 32-bit index arithmetic (the host bounds 2 B S H); the row decomposition
+// and t / stride are the only divisions, each a float estimate + fix-up.
+// The anchor (fp16 I-frame of group g) comes from the new tokens when that
+// I-frame is appended by this call (the same fp16 value the cache will
+// hold), else from the cache, so the waves of one launch never depend on
+// each other.
 template <int DT>
-__global__ __launch_bounds__(256) void append_kernel(AppendArgs a) {
+__device__ __forceinline__ void load_append_row(const AppendArgs &a, int item, int per_comp,
+                                                TokenRow &r) {
   const int lane = threadIdx.x & 63;
-  // 32-bit index arithmetic (the host bounds 2 B S H); the row decomposition
-  // and t / stride are the only divisions, each a float estimate + fix-up
-  int item = (int)blockIdx.x * (int)(blockDim.x >> 6) + (int)(threadIdx.x >> 6);
-  const int per_comp = a.B * a.S * a.H;
-  if (item >= 2 * per_comp) return;  // wave-uniform
   const int ci = item >= per_comp ? 1 : 0;
   item -= ci * per_comp;
   const int bs = div_pos(item, a.H);
@@ -255,47 +273,219 @@ __global__ __launch_bounds__(256) void append_kernel(AppendArgs a) {
   const int s = bs - b * a.S;
 
   const cq_component &c = a.comp[ci];
-  const int D = a.D, W = a.W, E = dims_per_lane(D);
+  const int D = a.D, E = dims_per_lane(D);
   const int64_t off = a.offsets ? (int64_t)a.offsets[b] : a.offset;
   const int64_t t = off + s;
   const int stride = c.stride;
-  const int64_t g = (t < 0x7fffffff) ? (int64_t)div_pos((int)t, stride) : t / stride;
-  const int64_t bh = (int64_t)b * a.H + h;
+  const int64_t g = (t >= 0 && t < 0x7fffffff) ? (int64_t)div_pos((int)t, stride)
+                                               : (t < 0 ? -1 : t / stride);
+  r.ci = ci;
+  r.t = t;
+  r.g = g;
+  r.bh = (int64_t)b * a.H + h;
   const void *x = a.x[ci];
   const int64_t xrow = b * a.xs[ci][0] + h * a.xs[ci][1] + (int64_t)s * a.xs[ci][2];
-
-  float v[kMaxE];
-  if (a.vec) {  // one 32-bit load of this lane's 2 elements
-    const uint32_t u = ((const uint32_t *)x)[(xrow >> 1) + lane];
-    v[0] = DT == CQ_BF16 ? bf2f((uint16_t)(u & 0xffffu)) : h2f((uint16_t)(u & 0xffffu));
-    v[1] = DT == CQ_BF16 ? bf2f((uint16_t)(u >> 16)) : h2f((uint16_t)(u >> 16));
+  auto load_x = [&](int64_t row, float (&out)[kMaxE], bool to_f16) {
+    if (a.vec) {  // one 32-bit load of this lane's 2 elements
+      const uint32_t u = ((const uint32_t *)x)[(row >> 1) + lane];
+      const float lo = DT == CQ_BF16 ? bf2f((uint16_t)(u & 0xffffu)) : h2f((uint16_t)(u & 0xffffu));
+      const float hi = DT == CQ_BF16 ? bf2f((uint16_t)(u >> 16)) : h2f((uint16_t)(u >> 16));
+      out[0] = to_f16 ? h2f(f2h(lo)) : lo;
+      out[1] = to_f16 ? h2f(f2h(hi)) : hi;
 #pragma unroll
-    for (int i = 2; i < kMaxE; ++i) v[i] = 0.f;
-  } else {
+      for (int i = 2; i < kMaxE; ++i) out[i] = 0.f;
+    } else {
 #pragma unroll
-    for (int i = 0; i < kMaxE; ++i) {
-      const int dim = lane * E + i;
-      v[i] = (i < E && dim < D) ? Dt<DT>::load(x, xrow + dim) : 0.f;
+      for (int i = 0; i < kMaxE; ++i) {
+        const int dim = lane * E + i;
+        const float e = (i < E && dim < D) ? Dt<DT>::load(x, row + dim) : 0.f;
+        out[i] = to_f16 ? h2f(f2h(e)) : e;
+      }
     }
-  }
-
-  // Anchor = fp16 I-frame of group g: from the cache if it predates this
-  // call, else straight from the new tokens (same fp16 value), so the waves
-  // of one launch never depend on each other.
+  };
+  load_x(xrow, r.v, false);
   const int64_t ta = g * stride;
-  const bool an_given = t != ta && ta >= off;
-  float an[kMaxE];
+  if (t != ta && ta >= off)  // wave-uniform
+    load_x(b * a.xs[ci][0] + h * a.xs[ci][1] + (ta - off) * a.xs[ci][2], r.an, true);
+  else
+    load_cache_anchor(c, r.bh, g, lane, D, a.vec != 0, r.an);
+}
+
+// Rows per wave and iteration: their loads are all issued before the first
+// row is encoded.  (gfx9 counts loads and stores with one in-order counter,
+// so a wave taking one row at a time waited for each row's stores before
+// the next row's loads could be used: two round trips per row.)
+constexpr int kAppendRowsPerWave = 1;
+
+template <int DT>
+__global__ __launch_bounds__(256) void append_kernel(AppendArgs a) {
+  // Grid-stride over the rows: a bulk append has millions of rows, and one
+  // short-lived workgroup per 4 rows left the GPU waiting on workgroup
+  // launches (the host caps the grid).
+  const int lane = threadIdx.x & 63;
+  const int per_comp = a.B * a.S * a.H, total = 2 * per_comp;
+  const int waves = (int)gridDim.x * (int)(blockDim.x >> 6);
+  // the row indices are wave-uniform: keep them (and all index math) scalar
+  const int first = __builtin_amdgcn_readfirstlane((int)blockIdx.x * (int)(blockDim.x >> 6) +
+                                                   (int)(threadIdx.x >> 6));
+  for (int base = first; base < total; base += kAppendRowsPerWave * waves) {
+    TokenRow r[kAppendRowsPerWave];
 #pragma unroll
-  for (int i = 0; i < kMaxE; ++i) an[i] = 0.f;
-  if (an_given) {
-    const int64_t arow = b * a.xs[ci][0] + h * a.xs[ci][1] + (ta - off) * a.xs[ci][2];
+    for (int j = 0; j < kAppendRowsPerWave; ++j)
+      load_append_row<DT>(a, min(base + j * waves, total - 1), per_comp, r[j]);
 #pragma unroll
-    for (int i = 0; i < kMaxE; ++i) {
-      const int dim = lane * E + i;
-      an[i] = (i < E && dim < D) ? h2f(f2h(Dt<DT>::load(x, arow + dim))) : 0.f;
+    for (int j = 0; j < kAppendRowsPerWave; ++j)
+      if (base + j * waves < total) encode_token<DT>(a.comp[r[j].ci], r[j], lane, a.D, a.W);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// cq_append at head_dim 128 with 16-bit tokens: four rows per wave, one row
+// per 16 lanes, lane j of a row holding dims 8j .. 8j+7 (one 16-byte load of
+// the token and of its anchor, one packed word out).  The per-row work (the
+// absmax reductions over 16 lanes, the scale, the index arithmetic) is done
+// by the same instructions for four rows, where the one-row-per-wave kernel
+// spent them on one (the bulk append was bound by VALU issue at ~270
+// instructions per row).  Same arithmetic as codec_row / encode_token.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float row16_max(float v) {
+  v = fmaxf(v, dpp_f<kDppQuadXor1>(v));
+  v = fmaxf(v, dpp_f<kDppQuadXor2>(v));
+  v = fmaxf(v, dpp_f<kDppRowHalfMirror>(v));
+  return fmaxf(v, dpp_f<kDppRowMirror>(v));
+}
+
+template <int DT>
+__device__ __forceinline__ void unpack8_dt(uint4 u, bool f16, float (&f)[8]) {
+  const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint16_t lo = (uint16_t)(w[i] & 0xffffu), hi = (uint16_t)(w[i] >> 16);
+    f[2 * i] = (DT == CQ_BF16 && !f16) ? bf2f(lo) : h2f(lo);
+    f[2 * i + 1] = (DT == CQ_BF16 && !f16) ? bf2f(hi) : h2f(hi);
+  }
+}
+
+// codec_row over a 16-lane row, 8 dims per lane (D = 128).
+template <int DT>
+__device__ __forceinline__ float codec_row16(float (&d)[8], int bits, float dz, int (&code)[8]) {
+  using T = Dt<DT>;
+  const int half = (1 << bits) >> 1;
+  const float hm1 = (float)(half - 1);
+  const float eps = T::round(1e-10f);
+  float m = 0.f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) m = fmaxf(m, fabsf(d[i]));
+  const float amax = row16_max(m);
+  float scale = T::round(amax / hm1);
+  if (dz > 0.f) {  // uniform over the row's 16 lanes
+    const float thr = T::round(amax * T::round(dz));
+    float m2 = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      if (fabsf(d[i]) < thr) d[i] = 0.f;
+      m2 = fmaxf(m2, fabsf(d[i]));
+    }
+    const float amax_c = row16_max(m2);
+    const float amax_safe = (amax_c < eps) ? amax : amax_c;
+    scale = T::round(amax_safe / hm1);
+  }
+  const float scale_safe = (scale < eps) ? 1.0f : scale;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const float q = T::round(d[i] / scale_safe);
+    int c;
+    if (q != q) {
+      c = 0;
+    } else {
+      float r = rintf(q);  // round half to even
+      r = fminf(fmaxf(r, (float)(-half)), hm1);
+      c = (int)r;
+    }
+    if (scale < eps) c = 0;
+    code[i] = c;
+  }
+  return scale;
+}
+
+template <int DT>
+__global__ __launch_bounds__(256) void append_row4_kernel(AppendArgs a) {
+  const int lane = threadIdx.x & 63, j = lane & 15;
+  const int per_comp = a.B * a.S * a.H, total = 2 * per_comp;
+  const int waves = (int)gridDim.x * (int)(blockDim.x >> 6);
+  const int first = 4 * __builtin_amdgcn_readfirstlane((int)blockIdx.x * (int)(blockDim.x >> 6) +
+                                                       (int)(threadIdx.x >> 6));
+  for (int base = first; base < total; base += 4 * waves) {
+    const int item0 = base + (lane >> 4);  // this lane's row
+    const bool live = item0 < total;
+    int item = live ? item0 : total - 1;
+    const int ci = item >= per_comp ? 1 : 0;
+    item -= ci * per_comp;
+    const int bs = div_pos(item, a.H);
+    const int h = item - bs * a.H;
+    const int b = div_pos(bs, a.S);
+    const int s = bs - b * a.S;
+    // the row's component (rows of both can share a wave)
+    uint16_t *const kf = ci ? a.comp[1].keyframes : a.comp[0].keyframes;
+    uint32_t *const pk = ci ? a.comp[1].packed : a.comp[0].packed;
+    uint16_t *const sc = ci ? a.comp[1].scales : a.comp[0].scales;
+    const int64_t cap_kf = ci ? a.comp[1].cap_keyframes : a.comp[0].cap_keyframes;
+    const int64_t cap_pf = ci ? a.comp[1].cap_pframes : a.comp[0].cap_pframes;
+    const int stride = ci ? a.comp[1].stride : a.comp[0].stride;
+    const int bits = ci ? a.comp[1].delta_bits : a.comp[0].delta_bits;
+    const float dz = ci ? a.comp[1].dead_zone : a.comp[0].dead_zone;
+    const uint16_t *x = (const uint16_t *)(ci ? a.x[1] : a.x[0]);
+    const int64_t xs0 = ci ? a.xs[1][0] : a.xs[0][0], xs1 = ci ? a.xs[1][1] : a.xs[0][1],
+                  xs2 = ci ? a.xs[1][2] : a.xs[0][2];
+
+    const int64_t off = a.offsets ? (int64_t)a.offsets[b] : a.offset;
+    const int64_t t = off + s;
+    const int64_t g = (t >= 0 && t < 0x7fffffff) ? (int64_t)div_pos((int)t, stride)
+                                                 : (t < 0 ? -1 : t / stride);
+    const int64_t bh = (int64_t)b * a.H + h;
+    const int64_t ta = g * stride;
+    const bool iframe = t == ta;
+    const bool an_in = !iframe && ta >= off;  // anchor appended by this call
+    const int64_t gg = g < 0 ? 0 : (g >= cap_kf ? cap_kf - 1 : g);
+    const uint4 *xp = (const uint4 *)(x + b * xs0 + h * xs1 + (int64_t)s * xs2 + 8 * j);
+    const uint4 *ap = an_in ? (const uint4 *)(x + b * xs0 + h * xs1 + (ta - off) * xs2 + 8 * j)
+                            : (const uint4 *)(kf + (bh * cap_kf + gg) * 128 + 8 * j);
+    const uint4 xv = *xp, av = *ap;
+    float v[8], an[8];
+    unpack8_dt<DT>(xv, false, v);
+    unpack8_dt<DT>(av, !an_in, an);
+    if (an_in) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) an[i] = h2f(f2h(an[i]));  // the fp16 I-frame value
+    }
+    const bool ok = live && t >= 0 && g < cap_kf;
+    if (iframe) {
+      if (ok) {
+        uint32_t w[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) w[i] = (uint32_t)f2h(v[2 * i]) | ((uint32_t)f2h(v[2 * i + 1]) << 16);
+        *(uint4 *)(kf + (bh * cap_kf + g) * 128 + 8 * j) = uint4{w[0], w[1], w[2], w[3]};
+      }
+    } else {
+      float d[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) d[i] = Dt<DT>::round(v[i] - Dt<DT>::round(an[i]));
+      int code[8];
+      const float scale = codec_row16<DT>(d, bits, dz, code);
+      const int64_t slot = t - g - 1;
+      if (ok && slot < cap_pf) {
+        uint32_t word = 0;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          int u = code[i] + 8;
+          u = u < 0 ? 0 : (u > 15 ? 15 : u);
+          word |= (uint32_t)u << (4 * i);
+        }
+        pk[(bh * cap_pf + slot) * 16 + j] = word;
+        if (j == 0) sc[bh * cap_pf + slot] = f2h(scale);
+      }
     }
   }
-  encode_token<DT>(c, bh, t, g, v, an_given, an, lane, D, W, a.vec != 0);
 }
 
 // ---------------------------------------------------------------------------
@@ -335,6 +525,19 @@ __global__ __launch_bounds__(256) void rope_append_kernel(RopeAppendArgs a) {
   float x2 = Dt<DT>::load(a.qkv, (int64_t)row * 128 + lane + 64);
   const int64_t t = a.offsets ? (int64_t)a.offsets[b] : a.offset;
   if (a.lengths && h == 0 && lane == 0) a.lengths[b] = (int32_t)(t + 1);
+  // key / value rows: the anchor row's load goes out with the token's
+  const int ci = h >= a.nq + a.nkv ? 1 : 0;
+  const int hk = h - a.nq - ci * a.nkv;
+  TokenRow r;
+  r.ci = ci;
+  r.t = t;
+  r.bh = (int64_t)b * a.nkv + hk;
+  if (h >= a.nq) {
+    const cq_component &c = a.comp[ci];
+    r.g = (t >= 0 && t < 0x7fffffff) ? (int64_t)div_pos((int)t, c.stride)
+                                     : (t < 0 ? -1 : t / c.stride);
+    load_cache_anchor(c, r.bh, r.g, lane, 128, true, r.an);
+  }
   if (h < a.nq + a.nkv) {
     const bool is_q = h < a.nq;
     const void *w = is_q ? a.q_w : a.k_w;
@@ -361,17 +564,15 @@ __global__ __launch_bounds__(256) void rope_append_kernel(RopeAppendArgs a) {
   }
   // key or value row: to the codec's lane layout (lane holds dims 2 lane and
   // 2 lane + 1), from lanes 2 lane mod 64 and 2 lane + 1 mod 64 of the
-  // first (lane < 32) or second half
-  const int ci = h >= a.nq + a.nkv ? 1 : 0;
-  const int hk = h - a.nq - ci * a.nkv;
+  // first (lane < 32) or second half.  With one new token a P-frame's
+  // anchor is always in the cache.
   const int s0 = (2 * lane) & 63;
   const float a0 = __shfl(x1, s0, 64), a1 = __shfl(x1, s0 + 1, 64);
   const float b0 = __shfl(x2, s0, 64), b1 = __shfl(x2, s0 + 1, 64);
-  float v[kMaxE] = {lane < 32 ? a0 : b0, lane < 32 ? a1 : b1, 0.f, 0.f};
-  const float none[kMaxE] = {0.f, 0.f, 0.f, 0.f};
-  const cq_component &c = a.comp[ci];
-  const int64_t g = t < 0x7fffffff ? (int64_t)div_pos((int)t, c.stride) : t / c.stride;
-  encode_token<DT>(c, (int64_t)b * a.nkv + hk, t, g, v, false, none, lane, 128, a.W, true);
+  r.v[0] = lane < 32 ? a0 : b0;
+  r.v[1] = lane < 32 ? a1 : b1;
+  r.v[2] = r.v[3] = 0.f;
+  encode_token<DT>(a.comp[ci], r, lane, 128, a.W);
 }
 
 // ---------------------------------------------------------------------------
@@ -416,6 +617,8 @@ static int launch_status() {
 }
 
 static bool bits_ok(int bits) { return bits >= 2 && bits <= 4; }
+
+constexpr int64_t kAppendGroups = 16384;
 
 int validate_cache(const cq_cache_desc *c) {
   if (!c) return CQ_ERR_ARG;
@@ -526,7 +729,8 @@ int cq_append(const cq_cache_desc *cache, const void *keys, const int64_t *key_s
   a.D = cache->head_dim;
   a.W = (cache->head_dim + 7) / 8;
   const int64_t items = 2 * (int64_t)a.B * n_new * a.H;
-  if (items >= 0x7fffffff - 4) return CQ_ERR_SHAPE;  // 32-bit row indices in the kernel
+  // 32-bit row indices in the kernel (base + 3 * grid waves stays below 2^31)
+  if (items >= 0x7fffffff - (1 << 20)) return CQ_ERR_SHAPE;
   a.S = (int)n_new;
   // 16-bit dtype, D = 128 (2 elements per lane), unit element stride, even
   // row strides and 4-byte aligned bases: each lane loads its 2 elements at once
@@ -537,8 +741,27 @@ int cq_append(const cq_cache_desc *cache, const void *keys, const int64_t *key_s
           (((uintptr_t)keys | (uintptr_t)values) & 3) == 0;
   a.offsets = offsets;
   a.offset = offset;
-  const dim3 grid((unsigned)((items + 3) / 4)), block(256);
+  // at most kAppendGroups workgroups (8 resident generations of 4-wave
+  // groups on 256 CUs); each wave then takes kAppendRowsPerWave rows at a
+  // time, every (grid waves)-th row
+  const int64_t per_group = 4 * kAppendRowsPerWave;
+  const dim3 grid((unsigned)std::min<int64_t>((items + per_group - 1) / per_group, kAppendGroups)),
+      block(256);
   hipStream_t s = (hipStream_t)stream;
+  // head_dim 128, 16-bit tokens whose rows start 16-byte aligned, 16-byte
+  // aligned keyframe rows: four rows per wave
+  const bool row4 = (dtype == CQ_F16 || dtype == CQ_BF16) && a.D == 128 &&
+                    ((key_strides[0] | key_strides[1] | key_strides[2] | value_strides[0] |
+                      value_strides[1] | value_strides[2]) & 7) == 0 &&
+                    key_strides[2] >= 0 && value_strides[2] >= 0 &&
+                    (((uintptr_t)keys | (uintptr_t)values | (uintptr_t)cache->k.keyframes |
+                      (uintptr_t)cache->v.keyframes) & 15) == 0;
+  if (row4) {
+    const dim3 g4((unsigned)std::min<int64_t>((items + 15) / 16, kAppendGroups));
+    if (dtype == CQ_F16) append_row4_kernel<CQ_F16><<<g4, block, 0, s>>>(a);
+    else append_row4_kernel<CQ_BF16><<<g4, block, 0, s>>>(a);
+    return launch_status();
+  }
   switch (dtype) {
     case CQ_F16: append_kernel<CQ_F16><<<grid, block, 0, s>>>(a); break;
     case CQ_BF16: append_kernel<CQ_BF16><<<grid, block, 0, s>>>(a); break;
