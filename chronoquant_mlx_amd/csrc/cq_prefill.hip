@@ -414,11 +414,20 @@ void prefill_mfma_kernel(PrefillArgs a) {
         const uint4 kv = *(const uint4 *)&lds.k[16 * t + col][32 * s + 8 * kg];
         d = mfma32(__builtin_bit_cast(h8_t, kv), qf[s], d);
       }
+      // fp16 q: scores rounded to fp16 like the fallback's fp16 matmul (two
+      // per conversion).  sc stays in natural units: the log2 scaling is
+      // folded into the exponent's fma below, and the row max is scaled once
+      // (scaling by log2 e > 0 keeps the max).
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        // fp16 q: scores rounded to fp16 like the fallback's fp16 matmul
-        const float sv16 = Bf16 ? d[r] : (float)(_Float16)d[r];
-        sc[t][r] = sv16 * kLog2e;
+      for (int r = 0; r < 4; r += 2) {
+        if (Bf16) {
+          sc[t][r] = d[r];
+          sc[t][r + 1] = d[r + 1];
+        } else {
+          const h2_t s16 = h2_t{(_Float16)d[r], (_Float16)d[r + 1]};
+          sc[t][r] = (float)s16.x;
+          sc[t][r + 1] = (float)s16.y;
+        }
       }
     }
     // Keys past lim_all exist only in a tile's last blocks (a uniform branch).
@@ -435,7 +444,7 @@ void prefill_mfma_kernel(PrefillArgs a) {
       mx = fmaxf(mx, fmaxf(fmaxf(sc[t][0], sc[t][1]), fmaxf(sc[t][2], sc[t][3])));
     // ---- 3. online softmax (row max over the 4 lane groups of the column) -------
     mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64)) * kLog2e;  // log2 units, as m_run
     if (__any(mx > m_run + kTau)) {
       const float m_new = fmaxf(m_run, mx);
       const float f = (m_run == -INFINITY) ? 0.f : fast_exp2(m_run - m_new);
@@ -449,12 +458,18 @@ void prefill_mfma_kernel(PrefillArgs a) {
       m_run = m_new;
     }
     const float mref = (m_run == -INFINITY) ? 0.f : m_run;
+    const h2_t ones = {(_Float16)1.f, (_Float16)1.f};
     h2_t pp[4][2];
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
-      pp[t][0] = h2_t{(_Float16)fast_exp2(sc[t][0] - mref), (_Float16)fast_exp2(sc[t][1] - mref)};
-      pp[t][1] = h2_t{(_Float16)fast_exp2(sc[t][2] - mref), (_Float16)fast_exp2(sc[t][3] - mref)};
-      l_run += (float)pp[t][0].x + (float)pp[t][0].y + (float)pp[t][1].x + (float)pp[t][1].y;
+      // p = 2^(s log2 e - m) in one fma + exp; l sums the fp16 weights (the
+      // values P.V uses) in fp32, two per v_dot2_f32_f16
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        pp[t][u] = h2_t{(_Float16)fast_exp2(__builtin_fmaf(sc[t][2 * u], kLog2e, -mref)),
+                        (_Float16)fast_exp2(__builtin_fmaf(sc[t][2 * u + 1], kLog2e, -mref))};
+        l_run = __builtin_amdgcn_fdot2(pp[t][u], ones, l_run, false);
+      }
     }
     // ---- 4. O += P . V: K index 8kg + e = key 16(2P) + 4kg + e (e < 4) or
     // 16(2P+1) + 4kg + e - 4 --------------------------------------------------------
