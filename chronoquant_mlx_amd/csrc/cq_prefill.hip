@@ -325,9 +325,12 @@ void prefill_mfma_kernel(PrefillArgs a) {
   //   hold their 4-key groups swapped in pairs (vt_col), so that the P.V
   //   reads of rows r and r + 8, which share banks at 32 banks, touch
   //   different ones.
-  const bool kside = tid < kThreads / 2;  // wave-uniform
+  // the component is wave-uniform: keep it scalar, so that the buffer
+  // resources below are too (per-lane resources put every load in a
+  // compiler waterfall loop)
+  const int c = __builtin_amdgcn_readfirstlane(tid < kThreads / 2 ? 0 : 1);
+  const bool kside = c == 0;
   const int st = tid & (kThreads / 2 - 1);
-  const int c = kside ? 0 : 1;
   const int stride = a.stride[c];
   const float istride = a.inv_stride[c];
   const int lstride = __builtin_ctz(stride), mstride = stride - 1;
