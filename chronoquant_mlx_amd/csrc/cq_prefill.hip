@@ -380,9 +380,12 @@ void prefill_mfma_kernel(PrefillArgs a) {
     }
   };
 
+  // The staging registers are free once a block is rebuilt in LDS: the next
+  // block's loads go out right after that barrier, so their latency overlaps
+  // this block's products and softmax instead of stalling the next rebuild.
+  if (kb_lo < kb_hi) load_block(kb_lo * kKeys);
   for (int kb = kb_lo; kb < kb_hi; ++kb) {
     const int k0 = kb * kKeys;
-    load_block(k0);
     // ---- 1. rebuild the K (waves 0-7) or V (waves 8-15) block in LDS -----------
     if (kside) {
       const h2_t s2 = as_h2(r_s[0] * 0x10001u);
@@ -406,6 +409,7 @@ void prefill_mfma_kernel(PrefillArgs a) {
       }
     }
     __syncthreads();
+    if (kb + 1 < kb_hi) load_block(k0 + kKeys);  // uniform
 
     // ---- 2. S^T = K . Q^T: lane (col = row, kg) gets keys 16t + 4kg + r ---------
     float sc[4][4];
