@@ -127,6 +127,27 @@ __device__ __forceinline__ float wave_sum(float v) {
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
 }
 
+// max / sum of v and v of lane ^ 16 (lane ^ 32) without the LDS crossbar:
+// gfx950 v_permlane16_swap (v_permlane32_swap) of v with itself gives every
+// lane the values of its even and odd 16-lane row (lower and upper half), in
+// that order, so both lanes of a pair compute the same bits.
+__device__ __forceinline__ float xor16_max(float v) {
+  const auto q = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(q[0]), __uint_as_float(q[1]));
+}
+__device__ __forceinline__ float xor32_max(float v) {
+  const auto q = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(q[0]), __uint_as_float(q[1]));
+}
+__device__ __forceinline__ float xor16_sum(float v) {
+  const auto q = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(q[0]) + __uint_as_float(q[1]);
+}
+__device__ __forceinline__ float xor32_sum(float v) {
+  const auto q = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(q[0]) + __uint_as_float(q[1]);
+}
+
 // OR over aligned groups of N lanes (N = 2, 4 or 8), result in every lane.
 template <int N>
 __device__ __forceinline__ uint32_t group_or(uint32_t v) {

@@ -99,13 +99,9 @@ __device__ __forceinline__ void wave_lds_sync() {
 }
 
 __device__ __forceinline__ float shfl_max_kg(float v) {  // over the 4 lanes sharing lane&15
-  v = fmaxf(v, __shfl_xor(v, 16, 64));
-  return fmaxf(v, __shfl_xor(v, 32, 64));
+  return xor32_max(xor16_max(v));
 }
-__device__ __forceinline__ float shfl_sum_kg(float v) {
-  v += __shfl_xor(v, 16, 64);
-  return v + __shfl_xor(v, 32, 64);
-}
+__device__ __forceinline__ float shfl_sum_kg(float v) { return xor32_sum(xor16_sum(v)); }
 
 // K code word (8 nibbles) -> A operand: n * 2^-24 as fp16 denormals in the K
 // order {d0, d4, d1, d5, d2, d6, d3, d7} of the word's dims.

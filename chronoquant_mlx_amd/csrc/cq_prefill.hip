@@ -450,8 +450,7 @@ void prefill_mfma_kernel(PrefillArgs a) {
     for (int t = 0; t < 4; ++t)
       mx = fmaxf(mx, fmaxf(fmaxf(sc[t][0], sc[t][1]), fmaxf(sc[t][2], sc[t][3])));
     // ---- 3. online softmax (row max over the 4 lane groups of the column) -------
-    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-    mx = fmaxf(mx, __shfl_xor(mx, 32, 64)) * kLog2e;  // log2 units, as m_run
+    mx = xor32_max(xor16_max(mx)) * kLog2e;  // log2 units, as m_run
     if (__any(mx > m_run + kTau)) {
       const float m_new = fmaxf(m_run, mx);
       const float f = (m_run == -INFINITY) ? 0.f : fast_exp2(m_run - m_new);
@@ -495,8 +494,7 @@ void prefill_mfma_kernel(PrefillArgs a) {
   }
 
   // ---- output: lane (col = grouped dim 16dt + col, kg) holds rows 4kg + r -------
-  l_run += __shfl_xor(l_run, 16, 64);
-  l_run += __shfl_xor(l_run, 32, 64);
+  l_run = xor32_sum(xor16_sum(l_run));
   const int perm8[8] = {0, 2, 4, 6, 1, 3, 5, 7};
   if (a.nsplit > 1) {
     split_epilogue<Bf16>(a, b, h, tile, split, p0, m_run, l_run, acc);
