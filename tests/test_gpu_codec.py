@@ -95,6 +95,46 @@ def test_append_bulk_matches_oracle(case):
         assert_state_equal(cache, b, *build_oracle(k[b], v[b], **params))
 
 
+@pytest.mark.parametrize("H,chunks", [(3, None), (3, [1, 2, 100, 7, 1, 222]), (5, [37, 1, 295])])
+@pytest.mark.parametrize("dtype", ["f16", "bf16"])
+def test_append_rows_straddle_components(H, chunks, dtype):
+    # Head_dim 128 appends with 16-bit tokens encode four rows per wave
+    # (append_row4_kernel).  With B*S*H odd a wave's rows straddle the K / V
+    # boundary and mix I-frames, anchors appended by the same call and
+    # anchors already in the cache; odd chunk sizes move every boundary.
+    rng = np.random.default_rng(H * 7 + len(chunks or []))
+    B, T, D = 1, 333, 128
+    k = np.cumsum(rng.standard_normal((B, H, T, D)) * 0.2, axis=2).astype(np.float32)
+    v = np.cumsum(rng.standard_normal((B, H, T, D)) * 0.2, axis=2).astype(np.float32)
+    if dtype == "bf16":
+        k = N.bf16_bits_to_f32(N.f32_to_bf16_bits(k))
+        v = N.bf16_bits_to_f32(N.f32_to_bf16_bits(v))
+    else:
+        k, v = k.astype(np.float16), v.astype(np.float16)
+    params = dict(stride_k=64, stride_v=32, bits_k=4, bits_v=3, dz_v=0.05)
+    cache = build_gpu_cache(k, v, chunks=chunks, dtype=TORCH_DT[dtype], **params)
+    assert_state_equal(cache, 0, *build_oracle(k[0], v[0], dtype=dtype, **params))
+
+
+def test_append_strided_rows_take_the_one_row_path():
+    # Rows that do not start 16-byte aligned (a head_dim-128 slice of wider
+    # rows) go through append_kernel instead: the same cache state.
+    from chronoquant_mlx_amd import ChronoQuantCache
+    g = torch.Generator(device="cuda").manual_seed(5)
+    B, H, T, D = 2, 4, 200, 128
+    wide = torch.randn(2, B, H, T, D + 4, device="cuda", generator=g).half()
+    k, v = wide[0, ..., :D], wide[1, ..., :D]
+    assert k.stride(2) % 8 != 0
+    states = []
+    for kk, vv in ((k, v), (k.contiguous(), v.contiguous())):
+        c = ChronoQuantCache(stride_k=32, stride_v=8, dead_zone_v=0.05)
+        c.update_and_fetch(kk[:, :, :77], vv[:, :, :77])
+        c.update_and_fetch(kk[:, :, 77:], vv[:, :, 77:])
+        states.append(c.state)
+    for a, b in zip(*states):
+        assert torch.equal(a, b)
+
+
 def test_append_streaming_equals_bulk():
     rng = np.random.default_rng(9)
     B, H, T, D = 1, 8, 300, 128
