@@ -116,23 +116,50 @@ def test_append_rows_straddle_components(H, chunks, dtype):
     assert_state_equal(cache, 0, *build_oracle(k[0], v[0], dtype=dtype, **params))
 
 
-def test_append_strided_rows_take_the_one_row_path():
+@pytest.mark.parametrize("device_pos", [False, True])
+def test_append_strided_rows_take_the_one_row_path(device_pos):
     # Rows that do not start 16-byte aligned (a head_dim-128 slice of wider
-    # rows) go through append_kernel instead: the same cache state.
+    # rows) go through append_kernel instead of the four-row kernel: the
+    # same cache state.  B * H = 9 rows per token, so the four-row kernel's
+    # waves also straddle sequences; with device positions the sequences
+    # append at different offsets (sequences 1 and 2 rewrite earlier ones).
     from chronoquant_mlx_amd import ChronoQuantCache
     g = torch.Generator(device="cuda").manual_seed(5)
-    B, H, T, D = 2, 4, 200, 128
+    B, H, T, D = 3, 3, 200, 128
     wide = torch.randn(2, B, H, T, D + 4, device="cuda", generator=g).half()
     k, v = wide[0, ..., :D], wide[1, ..., :D]
     assert k.stride(2) % 8 != 0
-    states = []
+    caches = []
     for kk, vv in ((k, v), (k.contiguous(), v.contiguous())):
         c = ChronoQuantCache(stride_k=32, stride_v=8, dead_zone_v=0.05)
         c.update_and_fetch(kk[:, :, :77], vv[:, :, :77])
-        c.update_and_fetch(kk[:, :, 77:], vv[:, :, 77:])
-        states.append(c.state)
-    for a, b in zip(*states):
-        assert torch.equal(a, b)
+        if device_pos:
+            pos = torch.tensor([77, 70, 61], dtype=torch.int32, device="cuda")
+            c.bind_device_position(pos, T)
+            for s0 in range(77, T, 41):  # multi-token appends at per-sequence offsets
+                s1 = min(s0 + 41, T)
+                c.update_and_fetch(kk[:, :, s0:s1], vv[:, :, s0:s1])
+                pos += s1 - s0
+        else:
+            c.update_and_fetch(kk[:, :, 77:], vv[:, :, 77:])
+        caches.append(c)
+    if not device_pos:
+        for a, b in zip(caches[0].state, caches[1].state):
+            assert torch.equal(a, b)
+        return
+    # every written row: sequence b holds positions [0, T - shift_b)
+    from chronoquant_mlx_amd.cache import _num_keyframes, _num_pframes
+    for b, top in enumerate((T, T - 7, T - 16)):
+        for comp in ("k", "v"):
+            s = caches[0]._stride(comp)
+            nk, npf = _num_keyframes(top, s), _num_pframes(top, s)
+            for arr, n in ((caches[0]._kf, nk), (caches[0]._pk, npf), (caches[0]._sc, npf)):
+                other = {id(caches[0]._kf): caches[1]._kf, id(caches[0]._pk): caches[1]._pk,
+                         id(caches[0]._sc): caches[1]._sc}[id(arr)]
+                x, y = arr[comp][b, :, :n], other[comp][b, :, :n]
+                assert torch.equal(x.view(torch.int16) if x.element_size() == 2 else x.view(torch.int32),
+                                   y.view(torch.int16) if y.element_size() == 2 else y.view(torch.int32)), \
+                    (b, comp)
 
 
 def test_append_streaming_equals_bulk():
