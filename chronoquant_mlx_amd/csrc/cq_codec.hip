@@ -348,13 +348,6 @@ __global__ __launch_bounds__(256) void append_kernel(AppendArgs a) {
 // spent them on one (the bulk append was bound by VALU issue at ~270
 // instructions per row).  Same arithmetic as codec_row / encode_token.
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ float row16_max(float v) {
-  v = fmaxf(v, dpp_f<kDppQuadXor1>(v));
-  v = fmaxf(v, dpp_f<kDppQuadXor2>(v));
-  v = fmaxf(v, dpp_f<kDppRowHalfMirror>(v));
-  return fmaxf(v, dpp_f<kDppRowMirror>(v));
-}
-
 template <int DT>
 __device__ __forceinline__ void unpack8_dt(uint4 u, bool f16, float (&f)[8]) {
   const uint32_t w[4] = {u.x, u.y, u.z, u.w};

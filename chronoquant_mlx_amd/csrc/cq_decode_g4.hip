@@ -297,10 +297,7 @@ __global__ __launch_bounds__(kThreadsMfma) void decode_g4_kernel(DecodeArgs a) {
       // slab m is half m & 1 of pair m >> 1
       ((h4_t *)&Gs.q[m >> 1][hh])[m & 1] = h4_t{v[0], v[4], v[2], v[6]};
       ((h4_t *)&Gs.q[8 + (m >> 1)][hh])[m & 1] = h4_t{v[1], v[5], v[3], v[7]};
-      part += __shfl_xor(part, 1, 64);
-      part += __shfl_xor(part, 2, 64);
-      part += __shfl_xor(part, 4, 64);
-      part += __shfl_xor(part, 8, 64);
+      part = row16_sum(part);  // the 16 lanes m of head hh
       if (m == 0) Gs.s8[hh] = 8.f * part;
     } else if (tid < 128) {
       (&Gs.zero[0][0])[tid - 64] = h8_t{};
@@ -389,11 +386,9 @@ __global__ __launch_bounds__(kThreadsMfma) void decode_g4_kernel(DecodeArgs a) {
       const float mx = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
       if (__any(m_run == -INFINITY || mx > kTau)) {
         // chunk max of head hq: its lanes differ in jb (col bits 2, 3) and kg
-        float cm = mx;
-        cm = fmaxf(cm, __shfl_xor(cm, 4, 64));
-        cm = fmaxf(cm, __shfl_xor(cm, 8, 64));
-        cm = fmaxf(cm, __shfl_xor(cm, 16, 64));
-        cm = fmaxf(cm, __shfl_xor(cm, 32, 64));
+        // (lanes ^ 4 and ^ 8 by DPP rotations, ^ 16 and ^ 32 by permlane
+        // swaps: no LDS round trips on the first chunk's path)
+        const float cm = xor32_max(xor16_max(row16_mod4_max(mx)));
         const float mref = (m_run == -INFINITY) ? 0.f : m_run;
         const float m_new = fmaxf(m_run, mref + cm);
         const float f = (m_run == -INFINITY) ? 0.f : fast_exp2(m_run - m_new);

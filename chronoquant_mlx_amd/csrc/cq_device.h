@@ -94,6 +94,8 @@ enum : int {
   kDppRowMirror = 0x140,
   kDppRowBcast15 = 0x142,
   kDppRowBcast31 = 0x143,
+  kDppRowRor4 = 0x124,  // row_ror:4 (rotate within the 16-lane row)
+  kDppRowRor8 = 0x128,
 };
 
 template <int CTRL, int ROW_MASK = 0xf>
@@ -125,6 +127,27 @@ __device__ __forceinline__ float wave_sum(float v) {
   v += dpp_f<kDppRowBcast15, 0xa>(v);
   v += dpp_f<kDppRowBcast31, 0xc>(v);
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+
+// Over the 16 lanes of a row (the first four steps of wave_max / wave_sum):
+// every lane of the row gets the result, the sum with the same bits in
+// every lane (each step adds a pair of values in either order).
+__device__ __forceinline__ float row16_max(float v) {
+  v = fmaxf(v, dpp_f<kDppQuadXor1>(v));
+  v = fmaxf(v, dpp_f<kDppQuadXor2>(v));
+  v = fmaxf(v, dpp_f<kDppRowHalfMirror>(v));
+  return fmaxf(v, dpp_f<kDppRowMirror>(v));
+}
+__device__ __forceinline__ float row16_sum(float v) {
+  v += dpp_f<kDppQuadXor1>(v);
+  v += dpp_f<kDppQuadXor2>(v);
+  v += dpp_f<kDppRowHalfMirror>(v);
+  return v + dpp_f<kDppRowMirror>(v);
+}
+// Max over the 4 lanes of a row congruent to this lane mod 4.
+__device__ __forceinline__ float row16_mod4_max(float v) {
+  v = fmaxf(v, dpp_f<kDppRowRor4>(v));
+  return fmaxf(v, dpp_f<kDppRowRor8>(v));
 }
 
 // max / sum of v and v of lane ^ 16 (lane ^ 32) without the LDS crossbar:
