@@ -431,7 +431,8 @@ void prefill_mfma_kernel(PrefillArgs a) {
           sc[t][r] = d[r];
           sc[t][r + 1] = d[r + 1];
         } else {
-          const h2_t s16 = h2_t{(_Float16)d[r], (_Float16)d[r + 1]};
+          typedef float f2_t __attribute__((ext_vector_type(2)));
+          const h2_t s16 = __builtin_convertvector(f2_t{d[r], d[r + 1]}, h2_t);
           sc[t][r] = (float)s16.x;
           sc[t][r + 1] = (float)s16.y;
         }
