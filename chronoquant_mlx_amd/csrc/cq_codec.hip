@@ -1,9 +1,10 @@
 // cq_codec.hip — encode side of the ChronoQuant hot path on gfx950:
 // residual quantisation (codec), INT4 packing, the fused append (I-frame or
 // quantise+pack in place) and the fp16 reconstruction used by the fallback
-// attention path.  One wavefront per (token, kv head) row; the row absmax is
-// a DPP reduction; every floating-point op is rounded to the input dtype the
-// way the reference's MLX arrays round it.
+// attention path.  A (token, kv head) row is encoded by one wavefront, or at
+// head_dim 128 with 16-bit tokens by 16 lanes (four rows per wave); the row
+// absmax is a DPP reduction; every floating-point op is rounded to the input
+// dtype the way the reference's MLX arrays round it.
 #include <hip/hip_runtime.h>
 #include <math.h>
 
@@ -158,7 +159,9 @@ __global__ __launch_bounds__(256) void unpack_kernel(const uint32_t *__restrict_
 }
 
 // ---------------------------------------------------------------------------
-// cq_append: one wavefront per (component, b, new token s, kv head)
+// cq_append, one wavefront per (component, b, new token s, kv head) row (any
+// head_dim and dtype; head_dim 128 with 16-bit tokens takes
+// append_row4_kernel below)
 // ---------------------------------------------------------------------------
 struct AppendArgs {
   cq_component comp[2];
