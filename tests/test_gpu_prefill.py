@@ -105,14 +105,16 @@ def test_sdpa_routes_prefill_and_matches_fallback(mask):
                  what=f"mask={mask}")
 
 
+@pytest.mark.parametrize("params", [dict(stride_k=64, stride_v=32, bits_v=3, dz_v=0.05),
+                                    dict(stride_k=5, stride_v=12)])
 @pytest.mark.parametrize("causal", [True, False])
-def test_bf16_queries(causal):
+def test_bf16_queries(causal, params):
     # bf16 queries: q' = bf16(q * bf16(scale)), fp32 scores (the reference's
     # bf16 x fp16 promotion), bf16 output; against the oracle fallback on the
-    # same q' (exact in fp16) with scale 1
+    # same q' (exact in fp16) with scale 1.  Strides 5 / 12 take the
+    # float-reciprocal token -> anchor path.
     from chronoquant_mlx_amd.kernels import chronoquant_prefill_kernel
     B, H, G, T, L, D = 1, 2, 4, 700, 130, 128
-    params = dict(stride_k=64, stride_v=32, bits_v=3, dz_v=0.05)
     k, v = _data(21, B, H, T, D)
     q32 = np.random.default_rng(22).standard_normal((B, G * H, L, D)).astype(np.float32)
     cache = build_gpu_cache(k, v, **params)
