@@ -417,6 +417,9 @@ def main():
                     help="skip the end-to-end configs[4] model run")
     ap.add_argument("--e2e-only", action="store_true",
                     help="run only the configs[4] model and print its figures (for profiling)")
+    ap.add_argument("--prefill-only", action="store_true",
+                    help="run only the chunked-prefill measurement and print its figures "
+                         "(for profiling)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on exactly one GPU; --gpus must be 1 "
@@ -433,6 +436,10 @@ def main():
     dev = torch.device("cuda:0")
     if args.e2e_only:
         print(json.dumps({"c4": time_e2e(dev)}), flush=True)
+        return
+    if args.prefill_only:
+        print(json.dumps({"prefill": time_prefill(dev, torch.cuda.Stream(dev), args.steps)}),
+              flush=True)
         return
     stream = torch.cuda.Stream(dev)
     log(f"[bench] building {cfg.name} cache (T={cfg.T}, B={cfg.B})")
