@@ -12,6 +12,13 @@ file's metadata beside the layer's class name.
 
     save_prompt_cache("prompt.safetensors", caches, {"model": "..."})
     caches = load_prompt_cache("prompt.safetensors")
+
+Opt-in dense residuals (save_prompt_cache(..., dense=True)): a component
+whose residual codes have 2 or 3 bits stores them in the file as a bit stream
+of that width instead of the reference's INT4 lanes (3-bit: 48 instead of 64
+bytes per 128-dim row).  load_prompt_cache expands them back to INT4 lanes,
+so a loaded cache has the reference layout and every kernel path.  Such a
+file is this library's format only: the reference cannot read it.
 """
 from __future__ import annotations
 
@@ -23,6 +30,73 @@ from .cache import ChronoQuantCache
 from .host import KVCache
 
 _FORMAT = "chronoquant_mlx_amd.prompt_cache.v1"
+_CHUNK_ROWS = 1 << 16  # rows packed / unpacked at a time (bounds the bit expansion)
+
+
+def _u32_to_i64(words: torch.Tensor) -> torch.Tensor:
+    return words.view(torch.int32).to(torch.int64) & 0xFFFFFFFF
+
+
+def dense_pack(words: torch.Tensor, head_dim: int, bits: int) -> torch.Tensor:
+    """INT4-lane rows [..., W] (uint32; nibble i of word w = code(8w + i) + 8,
+    nibbles of dims >= head_dim 0) -> the codes of dims < head_dim as a
+    little-endian stream of `bits`-bit fields holding code + 2^(bits-1):
+    field d occupies stream bits [bits*d, bits*d + bits).  uint8 [...,
+    ceil(head_dim * bits / 8)].  Raises if a code is out of the bits' range."""
+    if bits not in (2, 3):
+        raise ValueError("dense residuals are 2 or 3 bits")
+    W, D = words.shape[-1], head_dim
+    lead = words.shape[:-1]
+    nbytes = (D * bits + 7) // 8
+    flat = words.reshape(-1, W)
+    out = torch.empty(flat.shape[0], nbytes, dtype=torch.uint8, device=words.device)
+    base = 8 - (1 << (bits - 1))
+    sh4 = 4 * torch.arange(8, device=words.device)
+    shb = torch.arange(bits, device=words.device)
+    sh8 = torch.arange(8, device=words.device)
+    for r0 in range(0, flat.shape[0], _CHUNK_ROWS):
+        w = _u32_to_i64(flat[r0:r0 + _CHUNK_ROWS])
+        nib = ((w[:, :, None] >> sh4) & 0xF).reshape(w.shape[0], W * 8)[:, :D]
+        vals = nib - base
+        if bool(((vals < 0) | (vals >= (1 << bits))).any()):
+            raise ValueError(f"a code does not fit {bits} bits")
+        stream = ((vals[:, :, None] >> shb) & 1).reshape(w.shape[0], D * bits)
+        stream = torch.nn.functional.pad(stream, (0, nbytes * 8 - D * bits))
+        out[r0:r0 + _CHUNK_ROWS] = ((stream.reshape(-1, nbytes, 8) << sh8).sum(-1)).to(torch.uint8)
+    return out.reshape(*lead, nbytes)
+
+
+def dense_unpack(stream: torch.Tensor, head_dim: int, bits: int) -> torch.Tensor:
+    """Inverse of dense_pack: uint8 [..., nbytes] -> uint32 INT4-lane rows
+    [..., ceil(head_dim / 8)] (pad nibbles 0)."""
+    D = head_dim
+    W = (D + 7) // 8
+    nbytes = stream.shape[-1]
+    if nbytes != (D * bits + 7) // 8:
+        raise ValueError("dense stream size does not match head_dim and bits")
+    lead = stream.shape[:-1]
+    flat = stream.reshape(-1, nbytes)
+    out = torch.empty(flat.shape[0], W, dtype=torch.int32, device=stream.device)
+    base = 8 - (1 << (bits - 1))
+    sh8 = torch.arange(8, device=stream.device)
+    shb = torch.arange(bits, device=stream.device)
+    sh4 = 4 * torch.arange(8, device=stream.device)
+    for r0 in range(0, flat.shape[0], _CHUNK_ROWS):
+        b = flat[r0:r0 + _CHUNK_ROWS].to(torch.int64)
+        bitv = ((b[:, :, None] >> sh8) & 1).reshape(b.shape[0], nbytes * 8)[:, :D * bits]
+        vals = (bitv.reshape(-1, D, bits) << shb).sum(-1)
+        nib = torch.nn.functional.pad(vals + base, (0, W * 8 - D))
+        word = (nib.reshape(-1, W, 8) << sh4).sum(-1)  # < 2^32
+        out[r0:r0 + _CHUNK_ROWS] = (word - ((word >> 31) << 32)).to(torch.int32)
+    return out.view(torch.uint32).reshape(*lead, W)
+
+
+def _dense_bits(c) -> dict:
+    """State index -> residual bits of each 2- or 3-bit packed component."""
+    bits = {2: int(c.delta_bits_k), 4: int(c._get_codec_for_v().delta_bits)}
+    return {i: b for i, b in bits.items() if b in (2, 3)}
+
+
 _PARAMS = ("stride_k", "stride_v", "delta_bits_k", "delta_bits_v", "dead_zone_k", "dead_zone_v",
            "use_fused", "layer_idx")
 
@@ -36,14 +110,24 @@ def _layer_info(c) -> dict:
     raise TypeError(f"cannot save a cache of type {type(c).__name__}")
 
 
-def save_prompt_cache(file_name: str, cache: list, metadata: dict | None = None) -> None:
-    """Write every layer's state (device tensors are copied to the host)."""
+def save_prompt_cache(file_name: str, cache: list, metadata: dict | None = None,
+                      dense: bool = False) -> None:
+    """Write every layer's state (device tensors are copied to the host).
+    dense: store 2- and 3-bit residual codes at their width (opt-in; see the
+    module docstring)."""
     from safetensors.torch import save_file
     tensors = {}
-    for i, c in enumerate(cache):
-        for j, t in enumerate(c.state):
-            tensors[f"{i}.{j}"] = t.detach().contiguous().cpu()
     info = [_layer_info(c) for c in cache]
+    for i, c in enumerate(cache):
+        state = c.state
+        packed = _dense_bits(c) if dense and isinstance(c, ChronoQuantCache) and state else {}
+        for j, t in enumerate(state):
+            if j in packed:
+                t = dense_pack(t.detach().contiguous(), c.head_dim, packed[j])
+            tensors[f"{i}.{j}"] = t.detach().contiguous().cpu()
+        if packed:
+            info[i]["dense"] = {"head_dim": int(c.head_dim),
+                                "bits": {str(j): b for j, b in packed.items()}}
     meta = {"format": _FORMAT, "layers": json.dumps(info),
             "n_state": json.dumps([len(c.state) for c in cache]),
             "metadata": json.dumps(metadata or {})}
@@ -64,6 +148,10 @@ def load_prompt_cache(file_name: str, return_metadata: bool = False, device: str
     caches = []
     for i, (layer, n) in enumerate(zip(info, n_state)):
         state = [tensors[f"{i}.{j}"] for j in range(n)]
+        dense = layer.get("dense")
+        if dense:
+            for j, b in dense["bits"].items():
+                state[int(j)] = dense_unpack(state[int(j)], dense["head_dim"], b)
         if layer["class"] == "ChronoQuantCache":
             c = ChronoQuantCache(**layer["params"], per_layer_v_bits=layer.get("per_layer_v_bits"))
         elif layer["class"] == "KVCache":

@@ -80,3 +80,29 @@ def test_mixed_cache_kinds(tmp_path):
     _same_state(a, a2)
     assert isinstance(p2, KVCache) and p2.offset == T
     assert torch.equal(p2.state[0].cpu(), p.state[0].cpu())
+
+
+@pytest.mark.parametrize("params", [dict(stride_k=64, stride_v=32, bits_v=3, dz_v=0.05),
+                                    dict(stride_k=16, stride_v=8, bits_k=2, bits_v=3),
+                                    dict(stride_k=32, stride_v=8)])
+def test_dense_file_reloads_the_same_cache(tmp_path, params):
+    # dense=True stores 2-/3-bit residual codes at their width; the reloaded
+    # cache has the INT4-lane layout again, bit-identical, and attends alike
+    import os
+
+    from chronoquant_mlx_amd import load_prompt_cache, save_prompt_cache
+    from chronoquant_mlx_amd.kernels import chronoquant_sdpa_kernel
+    B, H, T, D = 2, 4, 400, 128
+    k, v = _kv(8, B, H, T, D)
+    a = build_gpu_cache(k, v, **params)
+    f_int4, f_dense = str(tmp_path / "int4.safetensors"), str(tmp_path / "dense.safetensors")
+    save_prompt_cache(f_int4, [a])
+    save_prompt_cache(f_dense, [a], dense=True)
+    b = load_prompt_cache(f_dense)[0]
+    _same_state(a, b)
+    n_pf = {c: int(a.state[i].shape[2]) * B * H for c, i in (("k", 2), ("v", 4))}
+    bits = {"k": params.get("bits_k", 4), "v": params.get("bits_v", 4)}
+    saved = sum(n_pf[c] * (64 - D * bits[c] // 8) for c in "kv" if bits[c] < 4)
+    assert os.path.getsize(f_int4) - os.path.getsize(f_dense) - saved in range(-256, 256)
+    q = to_gpu(np.random.default_rng(9).standard_normal((B, 4 * H, D)).astype(np.float16))
+    assert torch.equal(chronoquant_sdpa_kernel(q, a, D ** -0.5), chronoquant_sdpa_kernel(q, b, D ** -0.5))
