@@ -67,3 +67,17 @@ def test_dense_pack_rejects_out_of_range_codes():
         dense_pack(words, 16, 4)
     with pytest.raises(ValueError):
         dense_unpack(torch.zeros(2, 5, dtype=torch.uint8), 16, 3)   # 6 bytes expected
+
+
+def test_dense_pack_chunking_is_seamless(monkeypatch):
+    # rows are packed in chunks; a chunk size that does not divide the row
+    # count gives the same stream as one chunk
+    import chronoquant_mlx_amd.persist as persist
+    from oracle.np_oracle import pack_int4_codes
+    codes = _codes(np.random.default_rng(11), (4, 3, 9, 128), 3)
+    words = torch.from_numpy(pack_int4_codes(codes).view(np.int32)).view(torch.uint32)
+    whole = persist.dense_pack(words, 128, 3)
+    monkeypatch.setattr(persist, "_CHUNK_ROWS", 5)
+    assert torch.equal(persist.dense_pack(words, 128, 3), whole)
+    back = persist.dense_unpack(whole, 128, 3)
+    assert torch.equal(back.view(torch.int32), words.view(torch.int32))
