@@ -49,13 +49,19 @@ def chronoquant_sdpa(queries: torch.Tensor, keys, values, cache, scale: float, m
     update_and_fetch returned (attention reads the cache).
     """
     batch, n_q_heads, q_len, head_dim = queries.shape
+    # bound to device positions (a graph-captured decode loop): the host
+    # offset trails the device one, so only the fused decode reads the cache
+    bound = getattr(cache, "_dev_pos", None) is not None
     use_fused = (
         cache.use_fused
         and q_len == 1
-        and cache.offset > 0
+        and (cache.offset > 0 or bound)
         and head_dim <= MAX_FUSED_HEAD_DIM
         and (mask is None or (isinstance(mask, str) and mask == "causal"))
     )
+    if bound and not use_fused:
+        raise ValueError("a cache bound to device positions serves only the fused decode "
+                         "(one query token, mask None, use_fused)")
     if use_fused:
         q = queries.reshape(batch, n_q_heads, head_dim)
         out = chronoquant_sdpa_kernel(q, cache, scale, seq_lens=cache._dev_len)

@@ -51,19 +51,34 @@ def _num_pframes(num_tokens: int, stride: int) -> int:
 
 
 _WORKSPACES: dict = {}
+# Workspaces replaced by larger ones.  A captured HIP graph keeps the address
+# it was captured with, so a replaced workspace is never freed.
+_RETIRED: list = []
 
 
 def _shared_workspace(device: torch.device, nbytes: int) -> torch.Tensor:
-    """Zero-initialised decode workspace shared by the caches of one device.
+    """Zero-initialised split-K workspace of the decode and prefill kernels,
+    one per (device, stream): the caches that run on one stream share it.
 
-    The decode kernels leave its counters at zero, so it is reused without
-    clearing; calls that share it are ordered on one stream.
+    The kernels return its counters to zero, so it is reused without
+    clearing.  Calls on one stream are ordered, so they never overlap on
+    it; calls on another stream use another workspace.  It is sized (or
+    grown) only outside stream capture: capture a graph on a stream after
+    one eager call of the same shape on that stream.
     """
-    key = (device.type, device.index)
+    stream = torch.cuda.current_stream(device)
+    key = (device.index, stream.cuda_stream)
     ws = _WORKSPACES.get(key)
     if ws is None or ws.numel() < nbytes:
-        ws = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
-        _WORKSPACES[key] = ws
+        if torch.cuda.is_current_stream_capturing():
+            raise RuntimeError(
+                "ChronoQuant: the decode workspace of this stream must be sized before graph "
+                "capture; run one eager step of the same shape on the capturing stream first")
+        old = 0 if ws is None else ws.numel()
+        new = torch.zeros(max(nbytes, 1 << 20, 2 * old), dtype=torch.uint8, device=device)
+        if ws is not None:
+            _RETIRED.append(ws)
+        _WORKSPACES[key] = ws = new
     return ws
 
 
@@ -262,7 +277,9 @@ class ChronoQuantCache:
         ks = (ctypes.c_int64 * 3)(keys.stride(0), keys.stride(1), keys.stride(2))
         vs = (ctypes.c_int64 * 3)(values.stride(0), values.stride(1), values.stride(2))
         if self._dev_pos is not None:
-            # device positions: append at pos[b], decode reads pos[b] + S tokens
+            # device positions: append at pos[b], the fused decode reads
+            # pos[b] + S tokens (chronoquant_sdpa serves a bound cache with
+            # the fused decode only: its other paths read the host offset)
             _lib.call("cq_append", self._descriptor(), keys.data_ptr(), ks, values.data_ptr(), vs,
                       _lib.dtype_code(keys.dtype), S, self._dev_pos.data_ptr(), 0,
                       _lib.stream_of(keys))

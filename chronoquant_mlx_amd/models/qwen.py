@@ -276,9 +276,11 @@ class GraphDecoder:
         return nxt
 
     def capture(self, first_token: torch.Tensor):
-        """Warm up once (allocations happen outside the graph; the warm-up
-        writes the first decode position, which the first replay rewrites
-        identically), then capture one step."""
+        """Warm up once on the stream the graph is then captured on
+        (allocations, among them the stream's decode workspace, happen
+        outside the graph; the warm-up writes the first decode position,
+        which the first replay rewrites identically), then capture one
+        step."""
         pos0 = self.pos.clone()
         self.tok.copy_(first_token)
         side = torch.cuda.Stream()
@@ -288,9 +290,11 @@ class GraphDecoder:
         torch.cuda.current_stream().wait_stream(side)
         self.pos.copy_(pos0)
         self.tok.copy_(first_token)
+        side.wait_stream(torch.cuda.current_stream())
         self.graph = torch.cuda.CUDAGraph()
-        with torch.no_grad(), torch.cuda.graph(self.graph):
+        with torch.no_grad(), torch.cuda.graph(self.graph, stream=side):
             self.out = self._step()
+        torch.cuda.current_stream().wait_stream(side)
         self.pos.copy_(pos0)
         self.tok.copy_(first_token)
 
