@@ -45,14 +45,16 @@ def _rebind(fn) -> None:
 
 
 def apply_patch():
-    """Activate ChronoQuant SDPA patch. Idempotent (patch.py:18-33)."""
+    """Route the host framework's attention symbol to chronoquant_sdpa for
+    ChronoQuant caches (patch.py:18-33); calling it again changes nothing."""
     global _patched
     if _patched:
         return
     _base.scaled_dot_product_attention = _patched_sdpa
     _rebind(_patched_sdpa)
     _patched = True
-    print("ChronoQuant SDPA patch applied to all loaded model modules.")
+    print("chronoquant_mlx_amd: scaled_dot_product_attention now sends ChronoQuant caches "
+          "to the gfx950 kernels")
 
 
 def apply():
@@ -78,9 +80,11 @@ def create_chronoquant_caches(
     use_fused: bool = True,
     per_layer_v_bits: list = None,
 ):
-    """Create ChronoQuant caches for all KV cache slots in model (patch.py:46-78).
+    """Replace every plain KVCache slot of the model's prompt cache with a
+    ChronoQuantCache of these codec settings (patch.py:46-78).
 
-    per_layer_v_bits: optional list of V bit widths per layer, e.g. [4, 2, 2, ...]
+    per_layer_v_bits: value residual width by layer index (layers past the
+    end of the list take its last entry); None uses delta_bits_v everywhere.
     """
     caches = _base.make_prompt_cache(model)
     for index in range(len(caches)):
@@ -97,7 +101,7 @@ def create_chronoquant_caches(
                 use_fused=use_fused,
                 per_layer_v_bits=per_layer_v_bits,
             )
-            caches[index].layer_idx = index  # for per-layer lookup
+            caches[index].layer_idx = index  # selects its entry of per_layer_v_bits
     return caches
 
 
