@@ -15,6 +15,8 @@
  *   cqo_append_component      cache.py:87-129  (one sequence, H heads)
  *   cqo_reconstruct_component cache.py:131-156
  *   cqo_sdpa_fallback         attention.py:8-20 + 61-74 (reconstruct + dense SDPA)
+ *   cqo_sdpa_fallback_mask    the same with a boolean array mask (attention.py:18-19)
+ *   cqo_sdpa_fallback_bf16q   the same for bf16 queries (fp32 scores and weights)
  *   cqo_sdpa_fused            MSL kernels.py:79-228 (fp32 dequant, online softmax)
  *   cqo_sdpa_exact            textbook softmax attention in binary64 (closed form)
  * Arithmetic model: MLX evaluates fp16/bf16 elementwise ops with the result
@@ -301,12 +303,14 @@ void cqo_reconstruct_component(int H, int D, int64_t T, int stride,
 /* ------------------------------------------------------------------------ */
 /*
  * q: fp16 [nq][Tq][D]; rk, rv: fp16 [H][T][D]; out fp16 [nq][Tq][D].
- * causal != 0 applies the "causal" string mask (attention.py:12-16).
+ * causal != 0 applies the "causal" string mask (attention.py:12-16); mask
+ * (uint8 [Tq][T], may be NULL) is a boolean array mask (attention.py:18-19:
+ * where(mask, scores, finfo(fp16).min)), applied after the causal one.
  */
-void cqo_sdpa_fallback(const uint16_t *q, const uint16_t *rk,
-                       const uint16_t *rv, int nq, int H, int64_t Tq,
-                       int64_t T, int D, float scale, int causal,
-                       uint16_t *out) {
+void cqo_sdpa_fallback_mask(const uint16_t *q, const uint16_t *rk,
+                            const uint16_t *rv, int nq, int H, int64_t Tq,
+                            int64_t T, int D, float scale, int causal,
+                            const uint8_t *mask, uint16_t *out) {
   int rep = nq / H; /* attention.py:50 */
   float scale_h = cqo_h2f(cqo_f2h(scale));
 #pragma omp parallel
@@ -328,6 +332,7 @@ void cqo_sdpa_fallback(const uint16_t *q, const uint16_t *rk,
           for (int d = 0; d < D; ++d) s += (double)qs[d] * (double)cqo_h2f(kr[d]);
           float sf = cqo_h2f(cqo_f2h((float)s));
           if (causal && (T - Tq + i) < t) sf = -65504.0f; /* finfo(fp16).min */
+          if (mask && !mask[i * T + t]) sf = -65504.0f;
           sc[t] = sf;
           if (sf > mx) mx = sf;
         }
@@ -348,20 +353,86 @@ void cqo_sdpa_fallback(const uint16_t *q, const uint16_t *rk,
   }
 }
 
+void cqo_sdpa_fallback(const uint16_t *q, const uint16_t *rk,
+                       const uint16_t *rv, int nq, int H, int64_t Tq,
+                       int64_t T, int D, float scale, int causal,
+                       uint16_t *out) {
+  cqo_sdpa_fallback_mask(q, rk, rv, nq, H, Tq, T, D, scale, causal, NULL, out);
+}
+
+/*
+ * The same fallback for bf16 queries over the fp16 reconstruction.  MLX
+ * promotes bf16 x fp16 to fp32, so (attention.py:61-74): q_scaled =
+ * bf16(q * bf16(scale)) (:65, the weak scalar takes the array's dtype);
+ * scores = q_scaled @ k^T in fp32 (:70); masked entries take
+ * finfo(float32).min (:12-19); softmax(precise=True) in fp32 gives fp32
+ * weights (:72); weights @ v in fp32 (:73); one rounding to bf16 (:74).
+ * q: bf16 [nq][Tq][D]; out: bf16 [nq][Tq][D].
+ */
+void cqo_sdpa_fallback_bf16q(const uint16_t *q, const uint16_t *rk,
+                             const uint16_t *rv, int nq, int H, int64_t Tq,
+                             int64_t T, int D, float scale, int causal,
+                             const uint8_t *mask, uint16_t *out) {
+  int rep = nq / H;
+  float scale_b = cqo_bf2f(cqo_f2bf(scale));
+#pragma omp parallel
+  {
+    float *qs = (float *)malloc(sizeof(float) * D);
+    float *sc = (float *)malloc(sizeof(float) * (size_t)T);
+    double *acc = (double *)malloc(sizeof(double) * D);
+#pragma omp for collapse(2) schedule(static)
+    for (int j = 0; j < nq; ++j)
+      for (int64_t i = 0; i < Tq; ++i) {
+        int h = j / rep;
+        const uint16_t *qr = q + ((int64_t)j * Tq + i) * D;
+        for (int d = 0; d < D; ++d) qs[d] = cqo_bf2f(cqo_f2bf(cqo_bf2f(qr[d]) * scale_b));
+        float mx = -INFINITY;
+        for (int64_t t = 0; t < T; ++t) {
+          const uint16_t *kr = rk + ((int64_t)h * T + t) * D;
+          double s = 0.0;
+          for (int d = 0; d < D; ++d) s += (double)qs[d] * (double)cqo_h2f(kr[d]);
+          float sf = (float)s;
+          if ((causal && (T - Tq + i) < t) || (mask && !mask[i * T + t]))
+            sf = -3.4028234663852886e38f; /* finfo(float32).min */
+          sc[t] = sf;
+          if (sf > mx) mx = sf;
+        }
+        double den = 0.0;
+        for (int64_t t = 0; t < T; ++t) den += exp((double)sc[t] - (double)mx);
+        for (int d = 0; d < D; ++d) acc[d] = 0.0;
+        for (int64_t t = 0; t < T; ++t) {
+          float w = (float)(exp((double)sc[t] - (double)mx) / den);
+          const uint16_t *vr = rv + ((int64_t)h * T + t) * D;
+          for (int d = 0; d < D; ++d) acc[d] += (double)w * (double)cqo_h2f(vr[d]);
+        }
+        uint16_t *o = out + ((int64_t)j * Tq + i) * D;
+        for (int d = 0; d < D; ++d) o[d] = cqo_f2bf((float)acc[d]);
+      }
+    free(qs);
+    free(sc);
+    free(acc);
+  }
+}
+
 /* ------------------------------------------------------------------------ */
 /* MSL kernels.py:79-228 semantics: k = fp32(a) + fp32(c)*fp32(s), q' =      */
 /* fp32(fp16(q*scale)) (attention.py:46), output fp32.  Here the sums run in  */
 /* binary64 so this is the fused kernel's math without its summation order.  */
 /* ------------------------------------------------------------------------ */
-void cqo_sdpa_fused(const uint16_t *q, int nq, int H, int D, int64_t T,
-                    float scale, int stride_k, int stride_v,
-                    const uint16_t *kf_k, int64_t cap_kf_k, const uint32_t *pk_k,
-                    int64_t cap_pf_k, const uint16_t *sc_k,
-                    const uint16_t *kf_v, int64_t cap_kf_v, const uint32_t *pk_v,
-                    int64_t cap_pf_v, const uint16_t *sc_v, float *out) {
+/* absw (may be NULL): sum_t p_t |v_t| / sum_t p_t per output element, the
+ * scale of a weighted sum's rounding error (a kernel whose weights carry
+ * relative error u differs by at most u * absw). */
+void cqo_sdpa_fused_absw(const uint16_t *q, int nq, int H, int D, int64_t T,
+                         float scale, int stride_k, int stride_v,
+                         const uint16_t *kf_k, int64_t cap_kf_k, const uint32_t *pk_k,
+                         int64_t cap_pf_k, const uint16_t *sc_k,
+                         const uint16_t *kf_v, int64_t cap_kf_v, const uint32_t *pk_v,
+                         int64_t cap_pf_v, const uint16_t *sc_v, float *out, float *absw) {
   int rep = nq / H;
   int W = (D + 7) / 8;
   float scale_h = cqo_h2f(cqo_f2h(scale));
+  /* q heads are independent: one per thread (same sums in the same order) */
+#pragma omp parallel for schedule(dynamic, 1)
   for (int j = 0; j < nq; ++j) {
     int h = j / rep;
     double *sc = (double *)malloc(sizeof(double) * (size_t)T);
@@ -386,6 +457,7 @@ void cqo_sdpa_fused(const uint16_t *q, int nq, int H, int D, int64_t T,
     }
     double den = 0.0;
     double *o = (double *)calloc((size_t)D, sizeof(double));
+    double *oa = (double *)calloc((size_t)D, sizeof(double));
     for (int64_t t = 0; t < T; ++t) {
       double p = exp(sc[t] - mx);
       den += p;
@@ -400,12 +472,26 @@ void cqo_sdpa_fused(const uint16_t *q, int nq, int H, int D, int64_t T,
           vv = vv + (float)c * s;
         }
         o[d] += p * (double)vv;
+        oa[d] += p * fabs((double)vv);
       }
     }
     for (int d = 0; d < D; ++d) out[(int64_t)j * D + d] = (float)(den > 0 ? o[d] / den : 0.0);
+    if (absw)
+      for (int d = 0; d < D; ++d) absw[(int64_t)j * D + d] = (float)(den > 0 ? oa[d] / den : 0.0);
     free(o);
+    free(oa);
     free(sc);
   }
+}
+
+void cqo_sdpa_fused(const uint16_t *q, int nq, int H, int D, int64_t T,
+                    float scale, int stride_k, int stride_v,
+                    const uint16_t *kf_k, int64_t cap_kf_k, const uint32_t *pk_k,
+                    int64_t cap_pf_k, const uint16_t *sc_k,
+                    const uint16_t *kf_v, int64_t cap_kf_v, const uint32_t *pk_v,
+                    int64_t cap_pf_v, const uint16_t *sc_v, float *out) {
+  cqo_sdpa_fused_absw(q, nq, H, D, T, scale, stride_k, stride_v, kf_k, cap_kf_k, pk_k,
+                      cap_pf_k, sc_k, kf_v, cap_kf_v, pk_v, cap_pf_v, sc_v, out, NULL);
 }
 
 /* Textbook attention in binary64: out[j] = sum_t softmax(q'_j . k_t) v_t, */

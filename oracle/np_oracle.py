@@ -174,8 +174,9 @@ class Component:
 
 
 def sdpa_fallback(q: np.ndarray, rk: np.ndarray, rv: np.ndarray, scale: float,
-                  causal: bool = False) -> np.ndarray:
-    """attention.py:61-74 for fp16 inputs.  q [nq, Tq, D]; rk/rv [H, T, D]."""
+                  causal: bool = False, mask: np.ndarray | None = None) -> np.ndarray:
+    """attention.py:61-74 for fp16 inputs.  q [nq, Tq, D]; rk/rv [H, T, D];
+    mask: optional boolean array [Tq, T] (attention.py:18-19)."""
     nq, Tq, D = q.shape
     H, T, _ = rk.shape
     rep = nq // H
@@ -187,6 +188,8 @@ def sdpa_fallback(q: np.ndarray, rk: np.ndarray, rv: np.ndarray, scale: float,
         qi = np.arange(T - Tq, T)[:, None]
         ki = np.arange(T)[None, :]
         s = np.where(qi >= ki, s, np.float32(np.finfo(np.float16).min))
+    if mask is not None:
+        s = np.where(np.asarray(mask, bool), s, np.float32(np.finfo(np.float16).min))
     m = s.max(axis=-1, keepdims=True).astype(np.float64)
     e = np.exp(s.astype(np.float64) - m)
     w = (e / e.sum(axis=-1, keepdims=True)).astype(np.float16)

@@ -39,8 +39,12 @@ def lib() -> ctypes.CDLL:
         L.cqo_append_component.restype = I32
         L.cqo_reconstruct_component.argtypes = [I32, I32, I64, I32, P, I64, P, I64, P, P]
         L.cqo_sdpa_fallback.argtypes = [P, P, P, I32, I32, I64, I64, I32, F, I32, P]
+        L.cqo_sdpa_fallback_mask.argtypes = [P, P, P, I32, I32, I64, I64, I32, F, I32, P, P]
+        L.cqo_sdpa_fallback_bf16q.argtypes = [P, P, P, I32, I32, I64, I64, I32, F, I32, P, P]
         L.cqo_sdpa_fused.argtypes = [P, I32, I32, I32, I64, F, I32, I32,
                                      P, I64, P, I64, P, P, I64, P, I64, P, P]
+        L.cqo_sdpa_fused_absw.argtypes = [P, I32, I32, I32, I64, F, I32, I32,
+                                          P, I64, P, I64, P, P, I64, P, I64, P, P, P]
         L.cqo_sdpa_exact.argtypes = [P, P, P, I32, I32, I64, I32, ctypes.c_double, P]
         L.cqo_decode_step.argtypes = [P, I32, I32, I32, I64, F, I32, I32,
                                       P, I64, P, I64, P, P, I64, P, I64, P, P, P, P]
@@ -182,30 +186,65 @@ class OracleComponent:
 
 
 def sdpa_fallback(q: np.ndarray, rk: np.ndarray, rv: np.ndarray, scale: float,
-                  causal: bool = False) -> np.ndarray:
-    """attention.py:61-74.  q fp16 [nq, Tq, D]; rk, rv fp16 [H, T, D]."""
+                  causal: bool = False, mask: np.ndarray | None = None) -> np.ndarray:
+    """attention.py:61-74.  q fp16 [nq, Tq, D]; rk, rv fp16 [H, T, D]; mask:
+    optional boolean array [Tq, T] (attention.py:18-19), on top of causal."""
     q = np.ascontiguousarray(q, np.float16).view(np.uint16)
     rk = np.ascontiguousarray(rk, np.float16).view(np.uint16)
     rv = np.ascontiguousarray(rv, np.float16).view(np.uint16)
     nq, Tq, D = q.shape
     H, T, _ = rk.shape
     out = np.empty((nq, Tq, D), np.uint16)
-    lib().cqo_sdpa_fallback(_p(q), _p(rk), _p(rv), nq, H, Tq, T, D, float(scale),
-                            int(causal), _p(out))
+    if mask is None:
+        lib().cqo_sdpa_fallback(_p(q), _p(rk), _p(rv), nq, H, Tq, T, D, float(scale),
+                                int(causal), _p(out))
+    else:
+        m = np.ascontiguousarray(np.broadcast_to(np.asarray(mask, bool), (Tq, T)), np.uint8)
+        lib().cqo_sdpa_fallback_mask(_p(q), _p(rk), _p(rv), nq, H, Tq, T, D, float(scale),
+                                     int(causal), _p(m), _p(out))
     return out.view(np.float16)
 
 
+def bf16_to_f32(bits: np.ndarray) -> np.ndarray:
+    """bf16 bit patterns -> float32 (exact)."""
+    return (np.asarray(bits, np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+def sdpa_fallback_bf16q(q_bits: np.ndarray, rk: np.ndarray, rv: np.ndarray, scale: float,
+                        causal: bool = False, mask: np.ndarray | None = None) -> np.ndarray:
+    """attention.py:61-74 with bf16 queries (MLX's bf16 x fp16 promotion:
+    fp32 scores and weights, bf16 output).  q_bits: bf16 bit patterns
+    [nq, Tq, D]; rk, rv fp16 [H, T, D].  Returns bf16 bit patterns."""
+    q = np.ascontiguousarray(q_bits, np.uint16)
+    rk = np.ascontiguousarray(rk, np.float16).view(np.uint16)
+    rv = np.ascontiguousarray(rv, np.float16).view(np.uint16)
+    nq, Tq, D = q.shape
+    H, T, _ = rk.shape
+    out = np.empty((nq, Tq, D), np.uint16)
+    m = None
+    if mask is not None:
+        m = np.ascontiguousarray(np.broadcast_to(np.asarray(mask, bool), (Tq, T)), np.uint8)
+    lib().cqo_sdpa_fallback_bf16q(_p(q), _p(rk), _p(rv), nq, H, Tq, T, D, float(scale),
+                                  int(causal), None if m is None else _p(m), _p(out))
+    return out
+
+
 def sdpa_fused(q: np.ndarray, ck: OracleComponent, cv: OracleComponent,
-               scale: float) -> np.ndarray:
-    """MSL kernels.py:79-228 semantics.  q fp16 [nq, D] -> fp32 [nq, D]."""
+               scale: float, T: int | None = None, return_absw: bool = False):
+    """MSL kernels.py:79-228 semantics over the first T tokens (default: all
+    appended).  q fp16 [nq, D] -> fp32 [nq, D]; with return_absw also the
+    softmax-weighted mean of |v| per element, (out, absw)."""
     q = np.ascontiguousarray(q, np.float16).view(np.uint16)
     nq, D = q.shape
+    T = ck.offset if T is None else int(T)
+    assert 0 < T <= min(ck.offset, cv.offset)
     out = np.empty((nq, D), np.float32)
-    lib().cqo_sdpa_fused(_p(q), nq, ck.H, D, ck.offset, float(scale), ck.stride,
-                         cv.stride, _p(ck.kf), ck.cap_kf, _p(ck.pk), ck.cap_pf,
-                         _p(ck.sc), _p(cv.kf), cv.cap_kf, _p(cv.pk), cv.cap_pf,
-                         _p(cv.sc), _p(out))
-    return out
+    absw = np.empty((nq, D), np.float32) if return_absw else None
+    lib().cqo_sdpa_fused_absw(_p(q), nq, ck.H, D, T, float(scale), ck.stride,
+                              cv.stride, _p(ck.kf), ck.cap_kf, _p(ck.pk), ck.cap_pf,
+                              _p(ck.sc), _p(cv.kf), cv.cap_kf, _p(cv.pk), cv.cap_pf,
+                              _p(cv.sc), _p(out), None if absw is None else _p(absw))
+    return (out, absw) if return_absw else out
 
 
 def sdpa_exact(q: np.ndarray, k: np.ndarray, v: np.ndarray, scale: float) -> np.ndarray:

@@ -86,6 +86,51 @@ def assert_close(got, ref, atol=ATOL, rtol=RTOL, what=""):
     return float(err.max()), float(rel)
 
 
-def assert_tight(got, ref, what="", mfma=True):
+def assert_close_fallback(got, fb, exact, what=""):
+    """The fallback bar where the fallback's own rounding is large (c2's 8x
+    outlier channels): |got - fb| <= ATOL + RTOL*|fb| + |fb - exact|
+    elementwise, exact = binary64 attention over the same fp16
+    reconstruction, and relative L2 to the fallback <= RTOL.  The reference's
+    own fused kernel (kernels.py:79-228: fp32 dequant, fp32 scores) differs
+    from its fallback (fp16 reconstruction, fp16 scores and weights) by more
+    than ATOL + RTOL*|fb| on some c2 elements; both stay within the bar of
+    exact attention, so the fallback's distance to it is the slack."""
+    got = np.asarray(got, np.float64)
+    fb = np.asarray(fb, np.float64)
+    slack = np.abs(fb - np.asarray(exact, np.float64))
+    err = np.abs(got - fb)
+    bound = ATOL + RTOL * np.abs(fb) + slack
+    worst = np.unravel_index(np.argmax(err - bound), err.shape)
+    rel = np.linalg.norm(got - fb) / max(np.linalg.norm(fb), 1e-30)
+    assert np.all(err <= bound), (f"{what}: |d|={err[worst]:.3e} > {bound[worst]:.3e} at "
+                                  f"{tuple(int(i) for i in worst)} (fallback {fb[worst]:.4f}, "
+                                  f"its own error {slack[worst]:.3e})")
+    assert rel <= RTOL, f"{what} rel {rel:.3e} > {RTOL}"
+    return float(err.max()), float(rel)
+
+
+# With the softmax-weighted mean of |v| (absw, oracle.sdpa_fused) the MFMA
+# kernel's tight bar takes absw in place of |ref| in its relative part:
+# weights p and p*s_v carried in fp16 (relative error 2^-11 each) move a
+# weighted mean of v by a multiple of 2^-11 * absw, which is not small
+# against |ref| where the output cancels (c2's 8x outlier channels:
+# |ref| << absw).  The absolute part stays TIGHT_ATOL_MFMA: weights below
+# fp16's normal range carry an absolute error up to 2^-25 each, which over
+# tens of thousands of tokens no relative term bounds.  absw >= |ref|, so
+# elsewhere this is the |ref| bar.
+TIGHT_ATOL_ABSW, TIGHT_U_ABSW = 5e-4, 2.0 ** -9
+
+
+def assert_tight(got, ref, what="", mfma=True, absw=None):
+    if mfma and absw is not None:
+        got = np.asarray(got, np.float64)
+        ref = np.asarray(ref, np.float64)
+        err = np.abs(got - ref)
+        bound = TIGHT_ATOL_ABSW + TIGHT_U_ABSW * np.asarray(absw, np.float64)
+        worst = np.unravel_index(np.argmax(err - bound), err.shape)
+        assert np.all(err <= bound), (f"{what} (fused semantics, weighted-|v| bar): "
+                                      f"|d|={err[worst]:.3e} > {bound[worst]:.3e} at "
+                                      f"{tuple(int(i) for i in worst)} (ref {ref[worst]:.4f})")
+        return float(err.max()), 0.0
     atol, rtol = (TIGHT_ATOL_MFMA, TIGHT_RTOL_MFMA) if mfma else (TIGHT_ATOL, TIGHT_RTOL)
     return assert_close(got, ref, atol, rtol, what=what + " (fused semantics)")

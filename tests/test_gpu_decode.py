@@ -13,7 +13,8 @@ import pytest
 import torch
 
 from oracle import oracle as O
-from tests.cqtest import assert_close, assert_tight, build_gpu_cache, build_oracle, to_gpu
+from tests.cqtest import (assert_close, assert_close_fallback, assert_tight, build_gpu_cache,
+                          build_oracle, to_gpu)
 
 pytestmark = pytest.mark.gpu
 
@@ -29,7 +30,13 @@ def oracle_fallback(ck, cv, q_b, scale):
     return O.sdpa_fallback(q_b[:, None], ck.reconstruct(), cv.reconstruct(), scale)[:, 0]
 
 
-def run_config(name, T=None, B=None, generic=False, seqs=None):
+def run_config(name, T=None, B=None, generic=False, seqs=None, max_abs=None,
+               fallback_slack=False):
+    """Decode configuration `name` on the GPU and check sequences `seqs`
+    (default all) against the oracle; max_abs: also bound max |got - ref|
+    against the fallback by that value (the north star's plain max-abs);
+    fallback_slack: widen the fallback bar by the fallback's own distance to
+    binary64 attention (assert_close_fallback)."""
     from chronoquant_mlx_amd import synth
     cfg = synth.CONFIGS[name]
     B = cfg.B if B is None else B
@@ -43,24 +50,46 @@ def run_config(name, T=None, B=None, generic=False, seqs=None):
     for b in (range(B) if seqs is None else seqs):
         ck, cv = build_oracle(k[b], v[b], **params)
         ref = oracle_fallback(ck, cv, q[b], scale)
-        assert_close(out[b], ref, what=f"{name} b={b}")
-        assert_tight(out[b], O.sdpa_fused(q[b], ck, cv, scale), what=f"{name} b={b}",
-                     mfma=not generic)
+        if fallback_slack:
+            exact = O.sdpa_exact(q[b], ck.reconstruct(), cv.reconstruct(), scale)
+            err, _ = assert_close_fallback(out[b], ref, exact, what=f"{name} b={b}")
+            assert_close(out[b], exact, what=f"{name} b={b} vs binary64 attention")
+        else:
+            err, _ = assert_close(out[b], ref, what=f"{name} b={b}")
+        if max_abs is not None:
+            assert err <= max_abs, f"{name} b={b}: max-abs {err:.3e} > {max_abs}"
+        fused, absw = O.sdpa_fused(q[b], ck, cv, scale, return_absw=True)
+        if fallback_slack and not generic:
+            assert_tight(out[b], fused, what=f"{name} b={b}", absw=absw)
+        else:
+            assert_tight(out[b], fused, what=f"{name} b={b}", mfma=not generic)
 
 
+# c0 and c1 outputs stay well inside |o| < 1, so the north star's bar holds
+# there as a plain max-abs of 2e-3 as well as in the atol + rtol reading.
 @pytest.mark.parametrize("generic", [False, True])
 def test_c0_full(generic):
-    run_config("c0", generic=generic)
+    run_config("c0", generic=generic, max_abs=2e-3)
 
 
 @pytest.mark.parametrize("generic", [False, True])
 def test_c1_full(generic):
-    run_config("c1", generic=generic)
+    run_config("c1", generic=generic, max_abs=2e-3)
 
 
+# c2's 8x outlier channels make scores reach +-18, where the fallback's fp16
+# score rounding moves single elements by more than the bar; the reference's
+# own fused kernel differs from its fallback there too (assert_close_fallback)
 def test_c2_two_sequences():
-    # Full-Throttle V3, T = 32768: two of the eight sequences
-    run_config("c2", B=2)
+    # Full-Throttle V3, T = 32768: a batch of two (16 splits of 2048 tokens)
+    run_config("c2", B=2, fallback_slack=True)
+
+
+def test_c2_full_batch_plan():
+    # configs[2] at its own batch of 8: the plan bench.py times (4 splits of
+    # 8192 tokens per (sequence, kv head)); the first and the last sequence
+    # are checked against the oracle
+    run_config("c2", seqs=(0, 7), fallback_slack=True)
 
 
 @pytest.mark.parametrize("T", [1, 2, 31, 32, 33, 63, 64, 65, 129, 1000])

@@ -110,9 +110,10 @@ def test_sdpa_routes_prefill_and_matches_fallback(mask):
 @pytest.mark.parametrize("causal", [True, False])
 def test_bf16_queries(causal, params):
     # bf16 queries: q' = bf16(q * bf16(scale)), fp32 scores (the reference's
-    # bf16 x fp16 promotion), bf16 output; against the oracle fallback on the
-    # same q' (exact in fp16) with scale 1.  Strides 5 / 12 take the
-    # float-reciprocal token -> anchor path.
+    # bf16 x fp16 promotion), bf16 output; against the oracle's bf16-query
+    # fallback and, as a second reading, the fp16 fallback on the same q'
+    # (exact in fp16) with scale 1.  Strides 5 / 12 take the float-reciprocal
+    # token -> anchor path.
     from chronoquant_mlx_amd.kernels import chronoquant_prefill_kernel
     B, H, G, T, L, D = 1, 2, 4, 700, 130, 128
     k, v = _data(21, B, H, T, D)
@@ -123,8 +124,13 @@ def test_bf16_queries(causal, params):
     assert out.dtype == torch.bfloat16
     qprime = (qb.cpu() * torch.tensor(D ** -0.5, dtype=torch.bfloat16)).to(torch.float16).numpy()
     ck, cv = build_oracle(k[0], v[0], **params)
-    ref = O.sdpa_fallback(qprime[0], ck.reconstruct(), cv.reconstruct(), 1.0, causal=causal)
-    assert_close(out.float().cpu().numpy()[0], ref.astype(np.float64), what=f"causal={causal}")
+    rk, rv = ck.reconstruct(), cv.reconstruct()
+    ref = O.sdpa_fallback(qprime[0], rk, rv, 1.0, causal=causal)
+    got = out.float().cpu().numpy()[0]
+    assert_close(got, ref.astype(np.float64), what=f"causal={causal}")
+    qbits = qb.cpu().view(torch.int16).numpy().view(np.uint16)[0]
+    ref32 = O.bf16_to_f32(O.sdpa_fallback_bf16q(qbits, rk, rv, D ** -0.5, causal=causal))
+    assert_close(got, ref32.astype(np.float64), what=f"causal={causal} (bf16 fallback)")
 
 
 @pytest.mark.parametrize("bf16", [False, True])
