@@ -71,6 +71,7 @@ SIGNATURES = {
     "cq_reconstruct": ([_DESC, _I32, _I64, _P, _P], _I32),
     "cq_decode_workspace_size": ([_I32, _I32, _I32, _I32, _I64], _SZ),
     "cq_decode_attn": ([_DESC, _P, _I32, _I32, _F, _P, _I64, _I64, _P, _I32, _P, _SZ, _P], _I32),
+    "cq_decode_attn_noalloc": ([_DESC, _P, _I32, _I32, _F, _P, _I64, _I64, _P, _I32, _P], _I32),
     "cq_decode_attn_generic": ([_DESC, _P, _I32, _I32, _F, _P, _I64, _I64, _P, _I32, _P, _SZ, _P], _I32),
     "cq_fp16_decode_attn": ([_P, _P, _I64, _I32, _I32, _I32, _P, _I32, _I32, _F, _P, _I64, _I64,
                              _P, _I32, _P, _SZ, _P], _I32),

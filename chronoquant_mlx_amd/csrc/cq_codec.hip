@@ -649,6 +649,9 @@ const char *cq_status_string(int32_t status) {
     case CQ_ERR_WORKSPACE: return "workspace missing or too small";
     case CQ_ERR_UNSUPPORTED: return "unsupported configuration";
     case CQ_ERR_LAUNCH: return "kernel launch failed";
+    case CQ_ERR_SCRATCH:
+      return "shape needs more split workspace than the static scratch holds "
+             "(CQ_NOALLOC_SCRATCH_BYTES); use cq_decode_attn with a workspace";
     default: return "unknown status";
   }
 }

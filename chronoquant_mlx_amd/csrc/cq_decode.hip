@@ -10,6 +10,7 @@
 #include <algorithm>
 #include <atomic>
 #include <math.h>
+#include <mutex>
 
 #include "cq_decode_common.h"
 
@@ -305,6 +306,46 @@ static int decode_entry(const cq_cache_desc *cache, const void *q, int32_t q_dty
   return launch_generic(a, workspace, workspace_bytes, (hipStream_t)stream);
 }
 
+// ---------------------------------------------------------------------------
+// static scratch of cq_decode_attn_noalloc
+// ---------------------------------------------------------------------------
+// The split partials and counters of the allocation-free decode.  Each GPU
+// that loads this code object holds its own zero-filled copy until the
+// process ends; the decode kernels return the counters to zero after every
+// call.  In host code `scratch` names a host-side stand-in, never the device
+// copy: kernels receive the per-device address resolved below.
+constexpr size_t kScratchBytes = CQ_NOALLOC_SCRATCH_BYTES;
+__device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+constexpr int kMaxScratchDevices = 64;
+static std::atomic<void *> g_scratch[kMaxScratchDevices];
+static std::mutex g_scratch_mu;
+
+// Device address of the current device's scratch, resolved once per device.
+static int current_scratch(void **out) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) {
+    (void)hipGetLastError();
+    return CQ_ERR_LAUNCH;
+  }
+  if (dev < 0 || dev >= kMaxScratchDevices) return CQ_ERR_UNSUPPORTED;
+  void *p = g_scratch[dev].load(std::memory_order_acquire);
+  if (!p) {
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    p = g_scratch[dev].load(std::memory_order_relaxed);
+    if (!p) {
+      const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+      if (e != hipSuccess || !p) {
+        (void)hipGetLastError();
+        return CQ_ERR_LAUNCH;
+      }
+      g_scratch[dev].store(p, std::memory_order_release);
+    }
+  }
+  *out = p;
+  return CQ_OK;
+}
+
 }  // namespace cq
 
 using namespace cq;
@@ -337,6 +378,25 @@ int cq_decode_attn(const cq_cache_desc *cache, const void *q, int32_t q_dtype,
                    size_t workspace_bytes, cq_stream_t stream) {
   return decode_entry(cache, q, q_dtype, n_q_heads, scale, seq_lens, seq_len, max_seq_len, out,
                       out_dtype, workspace, workspace_bytes, stream, true);
+}
+
+int cq_decode_attn_noalloc(const cq_cache_desc *cache, const void *q, int32_t q_dtype,
+                           int32_t n_q_heads, float scale, const int32_t *seq_lens,
+                           int64_t seq_len, int64_t max_seq_len, void *out, int32_t out_dtype,
+                           cq_stream_t stream) {
+  int st = validate_cache(cache);
+  if (st) return st;
+  if (n_q_heads < 1 || seq_len < 0 || max_seq_len < 0) return CQ_ERR_ARG;
+  // the bound every plan of this shape fits in (the size cq_decode_workspace_size
+  // asks callers of cq_decode_attn for)
+  const size_t need = cq_decode_workspace_size(cache->batch, cache->n_kv_heads, n_q_heads,
+                                               cache->head_dim, seq_lens ? max_seq_len : seq_len);
+  if (need > kScratchBytes) return CQ_ERR_SCRATCH;
+  void *ws = nullptr;
+  st = current_scratch(&ws);
+  if (st) return st;
+  return decode_entry(cache, q, q_dtype, n_q_heads, scale, seq_lens, seq_len, max_seq_len, out,
+                      out_dtype, ws, kScratchBytes, stream, true);
 }
 
 int cq_fp16_decode_attn(const uint16_t *k, const uint16_t *v, int64_t cap_tokens,

@@ -42,7 +42,8 @@ enum cq_status {
   CQ_ERR_CAPACITY = 5,    /* append or read beyond the cache capacity */
   CQ_ERR_WORKSPACE = 6,   /* workspace missing or smaller than required */
   CQ_ERR_UNSUPPORTED = 7, /* valid request the library does not implement */
-  CQ_ERR_LAUNCH = 8       /* kernel launch reported an error */
+  CQ_ERR_LAUNCH = 8,      /* kernel launch reported an error */
+  CQ_ERR_SCRATCH = 9      /* shape needs more than the static scratch holds */
 };
 
 enum cq_dtype { CQ_F16 = 0, CQ_BF16 = 1, CQ_F32 = 2 };
@@ -140,6 +141,31 @@ int cq_decode_attn(const cq_cache_desc *cache, const void *q, int32_t q_dtype,
                    int64_t seq_len, int64_t max_seq_len, void *out,
                    int32_t out_dtype, void *workspace, size_t workspace_bytes,
                    cq_stream_t stream);
+
+/* Bytes of the static device scratch cq_decode_attn_noalloc works in (one
+ * array per GPU, held from the library's first use on that GPU until the
+ * process ends). */
+#define CQ_NOALLOC_SCRATCH_BYTES (32u << 20)
+
+/* cq_decode_attn without the workspace argument: the split partials and
+ * counters live in a static device array of CQ_NOALLOC_SCRATCH_BYTES per
+ * GPU instead of caller memory, so the call allocates nothing (no
+ * hipMalloc, no library allocation).  No counterpart in the reference: it is
+ * for callers that cannot allocate device memory (code under HIP graph
+ * capture, serving loops that forbid allocation).
+ * Same arguments, kernels and results as cq_decode_attn (bit-identical
+ * outputs).  A shape whose workspace (cq_decode_workspace_size) exceeds
+ * CQ_NOALLOC_SCRATCH_BYTES returns CQ_ERR_SCRATCH and launches nothing.
+ * Every call on one GPU shares that GPU's scratch: calls that overlap in
+ * time on one GPU (unordered streams, concurrent graph replays) race on it
+ * and must not be issued.  The counters in it start at zero and every call
+ * returns them to zero.  The first call on each GPU resolves the array's
+ * device address (hipGetSymbolAddress) and must be made outside stream
+ * capture. */
+int cq_decode_attn_noalloc(const cq_cache_desc *cache, const void *q, int32_t q_dtype,
+                           int32_t n_q_heads, float scale, const int32_t *seq_lens,
+                           int64_t seq_len, int64_t max_seq_len, void *out,
+                           int32_t out_dtype, cq_stream_t stream);
 
 /* Same contract as cq_decode_attn but always runs the portable (VALU) decode
  * kernel, for any head_dim <= 256 and q dtype; the test suite uses it to
