@@ -62,18 +62,15 @@ def _shared_workspace(device: torch.device, nbytes: int) -> torch.Tensor:
 
     The kernels return its counters to zero, so it is reused without
     clearing.  Calls on one stream are ordered, so they never overlap on
-    it; calls on another stream use another workspace.  It is sized (or
-    grown) only outside stream capture: capture a graph on a stream after
-    one eager call of the same shape on that stream.
+    it; calls on another stream use another workspace.  Under stream
+    capture a missing (or too small) workspace is allocated from the
+    graph's memory pool; its zero fill is a kernel captured with it, so every
+    replay starts from zeroed counters.
     """
     stream = torch.cuda.current_stream(device)
     key = (device.index, stream.cuda_stream)
     ws = _WORKSPACES.get(key)
     if ws is None or ws.numel() < nbytes:
-        if torch.cuda.is_current_stream_capturing():
-            raise RuntimeError(
-                "ChronoQuant: the decode workspace of this stream must be sized before graph "
-                "capture; run one eager step of the same shape on the capturing stream first")
         old = 0 if ws is None else ws.numel()
         new = torch.zeros(max(nbytes, 1 << 20, 2 * old), dtype=torch.uint8, device=device)
         if ws is not None:

@@ -10,6 +10,8 @@
 #include <algorithm>
 #include <atomic>
 #include <math.h>
+#include <stdlib.h>
+
 #include <mutex>
 
 #include "cq_decode_common.h"
@@ -212,6 +214,17 @@ static int lpt_log2_for(int W) {
   int l = 0;
   while ((1 << l) < W) ++l;
   return l;
+}
+
+int64_t split_tokens_override() {
+  static const int64_t v = [] {
+    const char *e = getenv("CQ_DECODE_SPLIT_TOKENS");
+    if (!e || !*e) return (int64_t)0;
+    char *end = nullptr;
+    const long long x = strtoll(e, &end, 10);
+    return (end && *end == 0 && x > 0 && x % 64 == 0 && x <= (1 << 24)) ? (int64_t)x : (int64_t)0;
+  }();
+  return v;
 }
 
 int64_t resident_workgroups(const void *kernel, int threads, int slot) {

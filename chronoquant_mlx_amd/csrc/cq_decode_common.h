@@ -259,6 +259,53 @@ __device__ __forceinline__ void merge_partials(const DecodeArgs &a, __amdgpu_buf
   }
 }
 
+// Buffer resources over the split partials (32-bit offsets: the host bounds
+// both arrays below 2^31 bytes).  Wave-uniform: per-lane resources would make
+// the compiler serialise every access over the distinct resources.
+__device__ __forceinline__ void partial_rsrcs(const DecodeArgs &a, __amdgpu_buffer_rsrc_t &racc,
+                                              __amdgpu_buffer_rsrc_t &rml) {
+  const uint32_t rows = (uint32_t)(a.B * a.nq * a.nsplit);
+  racc = make_rsrc(a.part_acc, rows * (uint32_t)a.D * 4u);
+  rml = make_rsrc(a.part_ml, rows * 8u);
+}
+
+// After a workgroup has issued its partial stores: wait for them and take a
+// ticket on the (sequence, kv head, chunk) counter.  True (for the whole
+// workgroup) in the last of the `live` workgroups, which then folds every
+// partial and resets the counter (*ctr).
+__device__ __forceinline__ bool split_ticket(const DecodeArgs &a, int b, int h, int chunk,
+                                             int live, uint32_t *&ctr) {
+  __shared__ int s_last;
+  __builtin_amdgcn_s_waitcnt(0);  // this thread's partial stores are complete
+  __syncthreads();
+  ctr = a.counters + ((int64_t)b * a.H + h) * a.n_chunks + chunk;
+  if (threadIdx.x == 0) {
+    const uint32_t prev =
+        __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    s_last = (prev == (uint32_t)(live - 1));
+  }
+  __syncthreads();
+  return s_last;
+}
+
+__device__ __forceinline__ void reset_ticket(uint32_t *ctr) {
+  if (threadIdx.x == 0) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// The split epilogue after a workgroup has issued its partial stores: the
+// ticket, and in the last of the `live` workgroups the fold of every partial
+// and the counter reset.  Called by the whole workgroup.
+__device__ __forceinline__ void combine_tail(const DecodeArgs &a, int b, int h, int chunk, int gn,
+                                             int live, bool vec, __amdgpu_buffer_rsrc_t racc,
+                                             __amdgpu_buffer_rsrc_t rml, int64_t bq0) {
+  uint32_t *ctr;
+  if (!split_ticket(a, b, h, chunk, live, ctr)) return;
+  // ---- last workgroup: fold the nsplit partials of every (head, 4 dims) ----
+  if (vec) merge_partials<true>(a, racc, rml, bq0, gn, live);
+  else merge_partials<false>(a, racc, rml, bq0, gn, live);
+  reset_ticket(ctr);
+}
+
 // Per-workgroup epilogue.  The workgroup's merged state for q heads
 // j0 .. j0+gn-1 of kv head h is in LDS: wm[j] (running max, log2 units),
 // wl[j] (sum of weights), wo[j*ostride + d] (unnormalised output).  `live`
@@ -291,12 +338,8 @@ __device__ __forceinline__ void finish_workgroup(const DecodeArgs &a, int b, int
     return;
   }
   const int nsplit = a.nsplit;
-  // One wave-uniform buffer resource per partial array (32-bit offsets: the
-  // host bounds both arrays below 2^31 bytes).  Per-lane resources would make
-  // the compiler serialise every access over the distinct resources.
-  const uint32_t rows = (uint32_t)(a.B * a.nq * nsplit);
-  const __amdgpu_buffer_rsrc_t racc = make_rsrc(a.part_acc, rows * (uint32_t)D * 4u);
-  const __amdgpu_buffer_rsrc_t rml = make_rsrc(a.part_ml, rows * 8u);
+  __amdgpu_buffer_rsrc_t racc, rml;
+  partial_rsrcs(a, racc, rml);
   // partials: (m, l) and o of this split, 16 bytes per access
   for (int u = tid; u < gn * nd4; u += nthr) {
     const int j = u / nd4, d0 = 4 * (u - j * nd4);
@@ -312,22 +355,7 @@ __device__ __forceinline__ void finish_workgroup(const DecodeArgs &a, int b, int
   }
 
   if (live == kGridLive) live = grid_live(a, seq_len_of(a, b));
-  __shared__ int s_last;
-  __builtin_amdgcn_s_waitcnt(0);  // this thread's partial stores are complete
-  __syncthreads();
-  uint32_t *ctr = a.counters + ((int64_t)b * a.H + h) * a.n_chunks + chunk;
-  if (tid == 0) {
-    const uint32_t prev =
-        __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    s_last = (prev == (uint32_t)(live - 1));
-  }
-  __syncthreads();
-  if (!s_last) return;
-
-  // ---- last workgroup: fold the nsplit partials of every (head, 4 dims) ----
-  if (vec) merge_partials<true>(a, racc, rml, bq0, gn, live);
-  else merge_partials<false>(a, racc, rml, bq0, gn, live);
-  if (tid == 0) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  combine_tail(a, b, h, chunk, gn, live, vec, racc, rml, bq0);
 }
 
 // ---------------------------------------------------------------------------
@@ -348,6 +376,12 @@ int64_t resident_workgroups(const void *kernel, int threads, int slot);
 int64_t mfma_max_resident();     // max over the MFMA-file kernels
 int64_t decode_max_resident();   // max over every decode kernel
 
+// Tokens per split forced by the environment variable CQ_DECODE_SPLIT_TOKENS
+// (a positive multiple of 64, read once per process; 0 when unset or
+// invalid).  A tuning knob for split-count sweeps: every grid plan then uses
+// splits of that length, and uniform batches keep the grid plan.
+int64_t split_tokens_override();
+
 // Splits of kSplitGranule-multiple length sized so that the whole grid
 // (groups workgroups per split) is resident at once: one generation of
 // workgroups, no tail of late starters.  At most kMaxSplits.
@@ -359,6 +393,7 @@ inline SplitPlan plan_splits(int64_t groups, int64_t max_T, int64_t target) {
   if (max_T <= 0) max_T = 1;
   int64_t len = (max_T + ns - 1) / ns;
   len = (len + kSplitGranule - 1) / kSplitGranule * kSplitGranule;
+  if (const int64_t forced = split_tokens_override()) len = forced;
   ns = (max_T + len - 1) / len;
   if (ns > kMaxSplits) {
     len = (max_T + kMaxSplits - 1) / kMaxSplits;

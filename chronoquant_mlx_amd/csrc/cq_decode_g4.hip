@@ -66,10 +66,162 @@ struct G4Stage {
   G4WaveScratch w[kWaves];
 };
 
+// The workgroup merge: every wave's unnormalised output tile and its (m, l)
+// per head, heads-major so that a thread reads the 8 waves' values of one
+// head as two 16-byte words.
+struct alignas(16) G4Merge {
+  float t[kWaves][kG4][kD];
+  float m[kG4][kWaves], l[kG4][kWaves];
+};
+
 union G4Lds {
   G4Stage s;
-  MergeScratch mg;
+  G4Merge mg;
 };
+
+// The last workgroup's fold of the `live` partials: thread (unit u, slice
+// sl) = (tid / 4, tid % 4) owns head u / 32, dims 4 (u % 32) .. +3, and
+// splits sl, sl + 4, ...; all of its loads ((m, l) pairs and 16-byte partial
+// vectors, kCombineBatch splits at a time) are in flight together, and the
+// 4 slices of a unit, adjacent lanes, fold with DPP quad permutes.
+__device__ __forceinline__ void merge_partials_g4(const DecodeArgs &a, __amdgpu_buffer_rsrc_t racc,
+                                                  __amdgpu_buffer_rsrc_t rml, int64_t bq0, int gn,
+                                                  int nsplit) {
+  constexpr int kSlices = 4;
+  static_assert(kThreadsMfma == kSlices * kG4 * (kD / 4), "one thread per (head, 4 dims, slice)");
+  const int tid = threadIdx.x;
+  const int u = tid >> 2, sl = tid & (kSlices - 1);
+  const int j = u >> 5, d0 = 4 * (u & 31);
+  const bool live_unit = j < gn;
+  const uint32_t row0 = (uint32_t)((bq0 + (live_unit ? j : 0)) * a.nsplit);
+  float M = -INFINITY, L = 0.f;
+  float o[4] = {0.f, 0.f, 0.f, 0.f};
+  for (int sp0 = sl; sp0 < nsplit; sp0 += kCombineBatch * kSlices) {
+    f2v_t ml[kCombineBatch];
+    f4v_t ov[kCombineBatch];
+#pragma unroll
+    for (int k = 0; k < kCombineBatch; ++k) {
+      // splits past the end re-read the last live split and are masked below
+      const uint32_t spo = row0 + (uint32_t)min(sp0 + k * kSlices, nsplit - 1);
+      ml[k] = load_dev2(rml, spo * 8u);
+      ov[k] = load_dev4(racc, (spo * (uint32_t)kD + (uint32_t)d0) * 4u);
+    }
+    float mb = M;
+#pragma unroll
+    for (int k = 0; k < kCombineBatch; ++k) {
+      if (sp0 + k * kSlices >= nsplit) ml[k].x = -INFINITY;
+      mb = fmaxf(mb, ml[k].x);
+    }
+    const float mref = (mb == -INFINITY) ? 0.f : mb;
+    const float f = (M == -INFINITY) ? 0.f : fast_exp2(M - mref);
+    L *= f;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) o[c] *= f;
+#pragma unroll
+    for (int k = 0; k < kCombineBatch; ++k) {
+      const float w = (ml[k].x == -INFINITY) ? 0.f : fast_exp2(ml[k].x - mref);
+      L += w * ml[k].y;
+      o[0] += w * ov[k].x;
+      o[1] += w * ov[k].y;
+      o[2] += w * ov[k].z;
+      o[3] += w * ov[k].w;
+    }
+    M = mb;
+  }
+  // the unit's 4 slices (lanes 4u .. 4u + 3)
+  float Mx = fmaxf(M, dpp_f<kDppQuadXor1>(M));
+  Mx = fmaxf(Mx, dpp_f<kDppQuadXor2>(Mx));
+  const float f = (M == -INFINITY) ? 0.f : fast_exp2(M - Mx);
+  L *= f;
+#pragma unroll
+  for (int c = 0; c < 4; ++c) o[c] *= f;
+  L += dpp_f<kDppQuadXor1>(L);
+  L += dpp_f<kDppQuadXor2>(L);
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    o[c] += dpp_f<kDppQuadXor1>(o[c]);
+    o[c] += dpp_f<kDppQuadXor2>(o[c]);
+  }
+  if (live_unit && sl == 0) {
+    const float inv = L > 0.f ? 1.f / L : 0.f;
+    const int64_t oi = (bq0 + j) * kD + d0;
+    if (a.out_dtype == CQ_F16) {
+      const h2v_t lo = h2v_t{(_Float16)(o[0] * inv), (_Float16)(o[1] * inv)};
+      const h2v_t hi = h2v_t{(_Float16)(o[2] * inv), (_Float16)(o[3] * inv)};
+      *(uint2 *)((uint16_t *)a.out + oi) =
+          uint2{__builtin_bit_cast(uint32_t, lo), __builtin_bit_cast(uint32_t, hi)};
+    } else {
+#pragma unroll
+      for (int c = 0; c < 4; ++c) store_any(a.out_dtype, a.out, oi + c, o[c] * inv);
+    }
+  }
+}
+
+// The workgroup merge and the split epilogue.  Lanes 0..15 of each wave hold
+// the wave's unnormalised output of heads r < gn, dims 8 col .. 8 col + 7
+// (o_val(nb, r)), and lanes col < 4 of them the running max and weight sum
+// of head col.  After one barrier each of the 512 threads folds one (head,
+// dim) element over the 8 waves with the log-sum-exp weights, then writes
+// the output (the workgroup holds the whole sequence) or stores its split
+// partial from registers and runs the split tail.
+template <typename OVal>
+__device__ __forceinline__ void merge_finish_g4(const DecodeArgs &a, G4Merge &M, int b, int h,
+                                                int gn, int slot, int live, float m_run,
+                                                float l_run, OVal o_val) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int col = lane & 15, kg = lane >> 4;
+  __syncthreads();  // the staging area becomes the merge area
+  if (kg == 0) {
+#pragma unroll
+    for (int r = 0; r < kG4; ++r) {
+      if (r < gn) {
+        float4 *dst = (float4 *)&M.t[wave][r][8 * col];
+        dst[0] = make_float4(o_val(0, r), o_val(1, r), o_val(2, r), o_val(3, r));
+        dst[1] = make_float4(o_val(4, r), o_val(5, r), o_val(6, r), o_val(7, r));
+      }
+    }
+    if (col < kG4) {
+      M.m[col][wave] = m_run;
+      M.l[col][wave] = l_run;
+    }
+  }
+  __syncthreads();
+  static_assert(kThreadsMfma == kG4 * kD, "one thread per (head, dim) of the merge");
+  const int hh = tid >> 7, d = tid & (kD - 1);
+  const int64_t bq0 = (int64_t)b * a.nq + h * a.G;
+  const bool single = live == kGridLive ? a.nsplit == 1 : live == 1;
+  __amdgpu_buffer_rsrc_t racc, rml;
+  if (!single) partial_rsrcs(a, racc, rml);
+  if (hh < gn) {
+    const float4 m0 = *(const float4 *)&M.m[hh][0], m1 = *(const float4 *)&M.m[hh][4];
+    const float4 l0 = *(const float4 *)&M.l[hh][0], l1 = *(const float4 *)&M.l[hh][4];
+    const float mw[kWaves] = {m0.x, m0.y, m0.z, m0.w, m1.x, m1.y, m1.z, m1.w};
+    const float lw[kWaves] = {l0.x, l0.y, l0.z, l0.w, l1.x, l1.y, l1.z, l1.w};
+    float mm = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) mm = fmaxf(mm, mw[w]);
+    float O = 0.f, L = 0.f;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) {
+      const float f = (mw[w] == -INFINITY) ? 0.f : fast_exp2(mw[w] - mm);
+      O += f * M.t[w][hh][d];
+      L += f * lw[w];
+    }
+    if (single) {
+      store_any(a.out_dtype, a.out, (bq0 + hh) * kD + d, L > 0.f ? O / L : 0.f);
+    } else {
+      const uint32_t row = (uint32_t)((bq0 + hh) * a.nsplit + slot);
+      store_dev1(racc, (row * (uint32_t)kD + (uint32_t)d) * 4u, O);
+      if (d == 0) store_dev2(rml, row * 8u, f2v_t{mm, L});
+    }
+  }
+  if (single) return;
+  if (live == kGridLive) live = grid_live(a, seq_len_of(a, b));
+  uint32_t *ctr;
+  if (!split_ticket(a, b, h, 0, live, ctr)) return;
+  merge_partials_g4(a, racc, rml, bq0, gn, live);
+  reset_ticket(ctr);
+}
 
 // K operand of the score product from two code words (slabs 2p, 2p + 1).  A
 // nibble enters as an fp16 denormal: bits 0-3 and 4-7 of each 16-bit half
@@ -264,8 +416,13 @@ __global__ __launch_bounds__(kThreadsMfma) void decode_g4_kernel(DecodeArgs a) {
         va[r] = bload128(r_kfv, ((uint32_t)min(gv_base + 4 * kg + r, gv_last) * 256u + 16u * col) | dead);
     };
 
-    // The first chunk's loads go out before the q table is built, so the two
-    // round trips overlap.
+    // Wave 0's q rows are requested first, then every wave's first chunk:
+    // the two round trips overlap, and the q table (and the barrier after
+    // it) waits for the q rows only, not for wave 0's chunk behind them.
+    uint4 q_raw = uint4{0u, 0u, 0u, 0u};
+    if (tid < 64 && (tid >> 4) < gn)
+      q_raw = *(const uint4 *)((const uint16_t *)a.q +
+                               ((int64_t)b * a.nq + h * a.G + (tid >> 4)) * kD + 8 * (tid & 15));
     int64_t c0l = t0 + (int64_t)wave * kChunk;
     const bool has_work = c0l < t1;
     // (balanced plan: zero-initialised; left undefined on a segment without
@@ -273,10 +430,11 @@ __global__ __launch_bounds__(kThreadsMfma) void decode_g4_kernel(DecodeArgs a) {
     // across the whole body)
     G4Buf bufA, bufB;
     if constexpr (kBalanced) bufA = bufB = G4Buf{};
-    if (has_work) {
-      stage((int)c0l, bufA);
-      stage_va((int)c0l);
-    }
+    // Unconditional, so that the count of loads in flight is the same on every
+    // path and the q table's wait covers the q rows only: a wave without work
+    // stages a chunk past the end (no traffic, zeros).
+    stage((int)min(c0l, t1), bufA);
+    stage_va((int)min(c0l, t1));
 
     // ---- q table: q' = fp16(q * fp16(scale)) (bf16 queries: bf16(q * bf16(scale)))
     // per (parity, slab pair, head) in the order unpack_pair gives a code
@@ -286,8 +444,7 @@ __global__ __launch_bounds__(kThreadsMfma) void decode_g4_kernel(DecodeArgs a) {
       h8_t v = {};
       float part = 0.f;
       if (hh < gn) {
-        const uint4 raw =
-            *(const uint4 *)((const uint16_t *)a.q + ((int64_t)b * a.nq + h * a.G + hh) * kD + 8 * m);
+        const uint4 raw = q_raw;
         const h8_t x = a.q_dtype == CQ_BF16 ? bf16x8_scaled_to_f16(raw, bf16_round(a.scale))
                                             : __builtin_bit_cast(h8_t, raw) * (_Float16)a.scale;
         v = x;
@@ -518,10 +675,10 @@ __global__ __launch_bounds__(kThreadsMfma) void decode_g4_kernel(DecodeArgs a) {
       sw[r] = __shfl(w_run, r, 64);  // lane r: head r
       sx[r] = __shfl(x_run, r, 64);
     }
-    // merge_and_finish reads (m, l) of head col from the lanes col < 4 of kg 0:
+    // merge_finish_g4 reads (m, l) of head col from the lanes col < 4 of kg 0:
     // head col's score lanes of block 0.  Code columns: x = 1032 + c (even nb,
     // weight p s) or 1152 + 16c (odd nb, weight p s / 16).
-    merge_and_finish(a, lds.mg, b, h, 0, 0, gn, slot, live, m_run, l_run, [&](int nb, int r) {
+    merge_finish_g4(a, lds.mg, b, h, gn, slot, live, m_run, l_run, [&](int nb, int r) {
       const float corr = (nb & 1) ? 1024.f * sx[r] + 8.f * sw[r] : 1032.f * sw[r];
       return acc[nb][r] - corr;
     });
@@ -561,7 +718,7 @@ int launch_decode_g4(DecodeArgs &a, void *workspace, size_t ws_bytes, hipStream_
     const SplitPlan g = plan_splits((int64_t)a.B * a.H, a.max_T, resident);
     const int64_t grid_units = g.split_len / kUnit;
     const int64_t bal_units = ((int64_t)a.B * n_max + P - 1) / P;
-    if (bal_units < grid_units) {
+    if (bal_units < grid_units && !split_tokens_override()) {
       balanced = true;
     } else {
       a.nsplit = g.nsplit;

@@ -639,7 +639,8 @@ int launch_decode_mfma(DecodeArgs &a, void *workspace, size_t ws_bytes, hipStrea
   if (!plain_mode(a)) {
     const SplitPlan g = plan_splits((int64_t)a.B * cols, a.max_T, resident);
     const int64_t bal_units = ((int64_t)a.B * n_max + P - 1) / P;
-    balanced = (a.seq_lens && a.B > 1) || bal_units < g.split_len / kUnit;
+    balanced = (a.seq_lens && a.B > 1) ||
+               (bal_units < g.split_len / kUnit && !split_tokens_override());
     // unit indices are 32-bit in the kernel
     if (balanced && (int64_t)a.B * n_max >= ((int64_t)1 << 31)) balanced = false;
   }

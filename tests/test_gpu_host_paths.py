@@ -115,3 +115,40 @@ def test_bound_cache_takes_only_the_fused_decode():
         chronoquant_sdpa(q.expand(1, G * H, 3, D).contiguous(), None, None, cache, D ** -0.5,
                          mask="causal")
     cache.bind_device_position(None)
+
+
+@pytest.mark.parametrize("prefill", [False, True])
+def test_torch_graph_recipe(prefill):
+    # torch's recipe: warm up on a side stream, capture with
+    # torch.cuda.graph(g) (torch's own capture stream, whose split workspace
+    # is then allocated under capture); replays with other library calls
+    # between them must each equal the eager result
+    from chronoquant_mlx_amd.kernels import chronoquant_prefill_kernel, chronoquant_sdpa_kernel
+    H, G, T, D = 8, 4, 3000, 128
+    k, v = _data(40 + prefill, H, T, D)
+    cache = build_gpu_cache(k, v, stride_k=32, stride_v=8)
+    rng = np.random.default_rng(41)
+    if prefill:
+        q = to_gpu(rng.standard_normal((1, G * H, 256, D)))
+        run = lambda: chronoquant_prefill_kernel(q, cache, D ** -0.5, causal=True)
+    else:
+        q = to_gpu(rng.standard_normal((1, G * H, D)))
+        run = lambda: chronoquant_sdpa_kernel(q, cache, D ** -0.5)
+    ref = run().clone()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        run()
+    torch.cuda.current_stream().wait_stream(side)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        out = run()
+    k2, v2 = _data(42, 2, 700, D)
+    other = build_gpu_cache(k2, v2, stride_k=16, stride_v=4)
+    q2 = to_gpu(rng.standard_normal((1, 8, D)))
+    for _ in range(3):
+        out.fill_(float("nan"))
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out.view(torch.int16), ref.view(torch.int16))
+        chronoquant_sdpa_kernel(q2, other, D ** -0.5)  # eager work between the replays
