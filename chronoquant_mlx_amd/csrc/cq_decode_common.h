@@ -42,6 +42,7 @@ struct DecodeArgs {
   float *part_ml;      // [B][nq][nsplit][2]  (m in log2 units, l)
   float *part_acc;     // [B][nq][nsplit][D]
   uint32_t *counters;  // [B][H][n_chunks]
+  uint32_t *flags;     // [B][H][nsplit] split-ready flags (GQA-4 kernel); null: tickets
   int nsplit;
   int64_t split_len;
   int lpt_log2;  // portable kernel: lanes per token = 1 << lpt_log2 (>= W)
@@ -405,13 +406,18 @@ inline SplitPlan plan_splits(int64_t groups, int64_t max_T, int64_t target) {
   return p;
 }
 
-// Workspace layout: a fixed 64 KiB counter region first (one uint32 per
-// (sequence, kv head, q-head chunk); the kernels return every counter to zero),
-// then the split partials, whose size varies with the split count.  Keeping
-// the counters at a fixed place means calls of different shapes sharing one
-// workspace never see each other's partials as counters.
-constexpr size_t kCounterRegion = 64 << 10;
-constexpr int64_t kMaxCounters = kCounterRegion / sizeof(uint32_t);
+// Workspace layout: a fixed 256 KiB region first, which the kernels return
+// to zero after every call: 64 KiB of split tickets (one uint32 per
+// (sequence, kv head, q-head chunk)) and 192 KiB of split-ready flags (one
+// uint32 per (sequence, kv head, split) of the GQA-4 kernel); then the split
+// partials, whose size varies with the split count.  Keeping the counters and
+// flags at a fixed place means calls of different shapes (and the prefill)
+// sharing one workspace never see each other's partials as counters.
+constexpr size_t kCounterBytes = 64 << 10;
+constexpr size_t kFlagBytes = 192 << 10;
+constexpr size_t kCounterRegion = kCounterBytes + kFlagBytes;
+constexpr int64_t kMaxCounters = kCounterBytes / sizeof(uint32_t);
+constexpr int64_t kMaxFlags = kFlagBytes / sizeof(uint32_t);
 
 inline size_t round256(size_t x) { return (x + 255) / 256 * 256; }
 
@@ -424,6 +430,7 @@ inline size_t workspace_bytes_for(int B, int nq, int D, int nsplit) {
 inline void carve_workspace(DecodeArgs &a, void *ws) {
   char *p = (char *)ws;
   a.counters = (uint32_t *)p;
+  a.flags = (int64_t)a.B * a.H * a.nsplit <= kMaxFlags ? (uint32_t *)(p + kCounterBytes) : nullptr;
   p += kCounterRegion;
   const size_t ml = (size_t)a.B * a.nq * a.nsplit * 2 * sizeof(float);
   a.part_ml = (float *)p;
@@ -449,7 +456,7 @@ inline int setup_workspace(DecodeArgs &a, void *workspace, size_t ws_bytes) {
     carve_workspace(a, workspace);
   } else {
     a.part_ml = a.part_acc = nullptr;
-    a.counters = nullptr;
+    a.counters = a.flags = nullptr;
   }
   return CQ_OK;
 }

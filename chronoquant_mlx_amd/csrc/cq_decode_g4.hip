@@ -157,6 +157,28 @@ __device__ __forceinline__ void merge_partials_g4(const DecodeArgs &a, __amdgpu_
   }
 }
 
+// Slot 0's wait for the split-ready flags fl[1 .. live-1]: wave 0 polls them
+// with device-scope loads (one per lane per round) until every flag is set,
+// sleeping between rounds; the other waves wait at the barrier.  The other
+// splits of the sequence are running workgroups of the same grid (the plans
+// launch one resident generation) that publish their partials without
+// waiting on anything, so the wait ends; kPollRounds bounds it regardless.
+constexpr int kPollRounds = 1 << 20;
+__device__ __forceinline__ void wait_split_flags(const uint32_t *fl, int live) {
+  if (threadIdx.x < 64) {
+    const int lane = threadIdx.x;
+    for (int round = 0; round < kPollRounds; ++round) {
+      bool ready = true;
+      for (int sp = 1 + lane; sp < live; sp += 64)
+        ready = ready && __hip_atomic_load(const_cast<uint32_t *>(fl) + sp, __ATOMIC_RELAXED,
+                                           __HIP_MEMORY_SCOPE_AGENT) != 0u;
+      if (__all(ready)) break;
+      __builtin_amdgcn_s_sleep(1);
+    }
+  }
+  __syncthreads();
+}
+
 // The workgroup merge and the split epilogue.  Lanes 0..15 of each wave hold
 // the wave's unnormalised output of heads r < gn, dims 8 col .. 8 col + 7
 // (o_val(nb, r)), and lanes col < 4 of them the running max and weight sum
@@ -217,6 +239,24 @@ __device__ __forceinline__ void merge_finish_g4(const DecodeArgs &a, G4Merge &M,
   }
   if (single) return;
   if (live == kGridLive) live = grid_live(a, seq_len_of(a, b));
+  if (a.flags) {
+    // Split-ready flags: every split but slot 0 publishes its partial and
+    // sets its flag; slot 0 waits for the flags and folds.  No atomics, so
+    // the splits of a sequence do not queue on one counter (their tickets
+    // arrive within about a microsecond of each other and serialise).
+    uint32_t *fl = a.flags + ((int64_t)b * a.H + h) * a.nsplit;
+    __builtin_amdgcn_s_waitcnt(0);  // this thread's partial stores are complete
+    __syncthreads();
+    if (slot != 0) {
+      if (tid == 0) __hip_atomic_store(fl + slot, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      return;
+    }
+    wait_split_flags(fl, live);
+    merge_partials_g4(a, racc, rml, bq0, gn, live);
+    for (int sp = 1 + tid; sp < live; sp += kThreadsMfma)
+      __hip_atomic_store(fl + sp, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return;
+  }
   uint32_t *ctr;
   if (!split_ticket(a, b, h, 0, live, ctr)) return;
   merge_partials_g4(a, racc, rml, bq0, gn, live);
