@@ -74,7 +74,9 @@ struct alignas(16) G4Merge {
   float m[kG4][kWaves], l[kG4][kWaves];
 };
 
-union G4Lds {
+// The merge area is separate from the staging area, so a wave writes its
+// tile as soon as its own chunks are done.
+struct G4Lds {
   G4Stage s;
   G4Merge mg;
 };
@@ -192,7 +194,6 @@ __device__ __forceinline__ void merge_finish_g4(const DecodeArgs &a, G4Merge &M,
                                                 float l_run, OVal o_val) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int col = lane & 15, kg = lane >> 4;
-  __syncthreads();  // the staging area becomes the merge area
   if (kg == 0) {
 #pragma unroll
     for (int r = 0; r < kG4; ++r) {
@@ -723,7 +724,7 @@ __global__ __launch_bounds__(kThreadsMfma) void decode_g4_kernel(DecodeArgs a) {
       return acc[nb][r] - corr;
     });
     if constexpr (!kBalanced) return;
-    __syncthreads();  // the next segment's staging reuses the merge area
+    __syncthreads();  // the next segment's merge reuses the merge area
   }
 }
 
