@@ -589,16 +589,20 @@ __global__ __launch_bounds__(kThreadsMfma) void decode_g4_kernel(DecodeArgs a) {
         const float cm = xor32_max(xor16_max(row16_mod4_max(mx)));
         const float mref = (m_run == -INFINITY) ? 0.f : m_run;
         const float m_new = fmaxf(m_run, mref + cm);
-        const float f = (m_run == -INFINITY) ? 0.f : fast_exp2(m_run - m_new);
-        l_run *= f;
-        w_run *= f;
-        x_run *= f;
+        // (a wave's first chunk: the sums and acc are still zero)
+        if (!__all(m_run == -INFINITY)) {
+          const float f = (m_run == -INFINITY) ? 0.f : fast_exp2(m_run - m_new);
+          l_run *= f;
+          w_run *= f;
+          x_run *= f;
+          // acc row 4kg + r holds head r (rows >= 4 repeat heads r, unused);
+          // lane r of every quad holds head r's factor
+          const float fr[4] = {dpp_f<kDppQuadBcast<0>>(f), dpp_f<kDppQuadBcast<1>>(f),
+                               dpp_f<kDppQuadBcast<2>>(f), dpp_f<kDppQuadBcast<3>>(f)};
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          // acc row 4kg + r holds head r (rows >= 4 repeat heads r, unused)
-          const float fr = __shfl(f, r, 64);
+          for (int r = 0; r < 4; ++r)
 #pragma unroll
-          for (int nb = 0; nb < 8; ++nb) acc[nb][r] *= fr;
+            for (int nb = 0; nb < 8; ++nb) acc[nb][r] *= fr[r];
         }
         const float shift = ((m_new == -INFINITY) ? 0.f : m_new) - mref;
 #pragma unroll
@@ -704,18 +708,21 @@ __global__ __launch_bounds__(kThreadsMfma) void decode_g4_kernel(DecodeArgs a) {
     }
 
     // ---- totals of head hq: its 16 lanes hold disjoint tokens ---------------------------
+    // (the lanes of a row by DPP rotations, the 4 rows by shuffles)
+    l_run = row16_mod4_sum(l_run);
+    w_run = row16_mod4_sum(w_run);
+    x_run = row16_mod4_sum(x_run);
 #pragma unroll
-    for (int x = 4; x < 64; x *= 2) {
+    for (int x = 16; x < 64; x *= 2) {
       l_run += __shfl_xor(l_run, x, 64);
       w_run += __shfl_xor(w_run, x, 64);
       x_run += __shfl_xor(x_run, x, 64);
     }
-    float sw[4], sx[4];
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      sw[r] = __shfl(w_run, r, 64);  // lane r: head r
-      sx[r] = __shfl(x_run, r, 64);
-    }
+    // lane r of every quad: head r
+    const float sw[4] = {dpp_f<kDppQuadBcast<0>>(w_run), dpp_f<kDppQuadBcast<1>>(w_run),
+                         dpp_f<kDppQuadBcast<2>>(w_run), dpp_f<kDppQuadBcast<3>>(w_run)};
+    const float sx[4] = {dpp_f<kDppQuadBcast<0>>(x_run), dpp_f<kDppQuadBcast<1>>(x_run),
+                         dpp_f<kDppQuadBcast<2>>(x_run), dpp_f<kDppQuadBcast<3>>(x_run)};
     // merge_finish_g4 reads (m, l) of head col from the lanes col < 4 of kg 0:
     // head col's score lanes of block 0.  Code columns: x = 1032 + c (even nb,
     // weight p s) or 1152 + 16c (odd nb, weight p s / 16).

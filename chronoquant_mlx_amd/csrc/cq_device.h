@@ -97,6 +97,9 @@ enum : int {
   kDppRowRor4 = 0x124,  // row_ror:4 (rotate within the 16-lane row)
   kDppRowRor8 = 0x128,
 };
+// quad_perm [r,r,r,r]: every lane reads lane r of its quad
+template <int R>
+constexpr int kDppQuadBcast = 0x55 * R;
 
 template <int CTRL, int ROW_MASK = 0xf>
 __device__ __forceinline__ float dpp_f(float v) {
@@ -148,6 +151,10 @@ __device__ __forceinline__ float row16_sum(float v) {
 __device__ __forceinline__ float row16_mod4_max(float v) {
   v = fmaxf(v, dpp_f<kDppRowRor4>(v));
   return fmaxf(v, dpp_f<kDppRowRor8>(v));
+}
+__device__ __forceinline__ float row16_mod4_sum(float v) {
+  v += dpp_f<kDppRowRor4>(v);
+  return v + dpp_f<kDppRowRor8>(v);
 }
 
 // max / sum of v and v of lane ^ 16 (lane ^ 32) without the LDS crossbar:
