@@ -43,6 +43,7 @@ struct DecodeArgs {
   float *part_acc;     // [B][nq][nsplit][D]
   uint32_t *counters;  // [B][H][n_chunks]
   uint32_t *flags;     // [B][H][nsplit] split-ready flags (GQA-4 kernel); null: tickets
+  uint32_t *recs;      // [B][H][nsplit][64 units] fold records (GQA-4 grid plan); null: unused
   int nsplit;
   int64_t split_len;
   int lpt_log2;  // portable kernel: lanes per token = 1 << lpt_log2 (>= W)
@@ -406,16 +407,25 @@ inline SplitPlan plan_splits(int64_t groups, int64_t max_T, int64_t target) {
   return p;
 }
 
-// Workspace layout: a fixed 256 KiB region first, which the kernels return
-// to zero after every call: 64 KiB of split tickets (one uint32 per
-// (sequence, kv head, q-head chunk)) and 192 KiB of split-ready flags (one
-// uint32 per (sequence, kv head, split) of the GQA-4 kernel); then the split
-// partials, whose size varies with the split count.  Keeping the counters and
-// flags at a fixed place means calls of different shapes (and the prefill)
-// sharing one workspace never see each other's partials as counters.
+// Workspace layout: a fixed region first, which the kernels return to zero
+// after every call: 64 KiB of split tickets (one uint32 per (sequence, kv
+// head, q-head chunk)), 192 KiB of split-ready flags (one uint32 per
+// (sequence, kv head, split) of the GQA-4 kernel) and 1.5 MiB of fold records
+// (the GQA-4 grid plan's split partials, zero until written); then the split
+// partials of the other plans, whose size varies with the split count.
+// Keeping the zero region at a fixed place means calls of different shapes
+// (and the prefill) sharing one workspace never see each other's partials as
+// counters, flags or records.
 constexpr size_t kCounterBytes = 64 << 10;
 constexpr size_t kFlagBytes = 192 << 10;
-constexpr size_t kCounterRegion = kCounterBytes + kFlagBytes;
+// Fold record: one (split, head, 8 dims) unit of a split partial, 12 words:
+// m, l, 2 unused, then the 8 unnormalised outputs, each stored as its bit
+// pattern + 1 so that a zero word means "not written yet".
+constexpr int kRecWords = 12;
+constexpr int kRecUnits = 64;  // 4 heads x 16 groups of 8 dims per (sequence, kv head, split)
+constexpr int64_t kMaxRecSplits = 512;  // (sequence, kv head, split) triples
+constexpr size_t kRecBytes = (size_t)kMaxRecSplits * kRecUnits * kRecWords * sizeof(uint32_t);
+constexpr size_t kCounterRegion = kCounterBytes + kFlagBytes + kRecBytes;
 constexpr int64_t kMaxCounters = kCounterBytes / sizeof(uint32_t);
 constexpr int64_t kMaxFlags = kFlagBytes / sizeof(uint32_t);
 
@@ -431,11 +441,17 @@ inline void carve_workspace(DecodeArgs &a, void *ws) {
   char *p = (char *)ws;
   a.counters = (uint32_t *)p;
   a.flags = (int64_t)a.B * a.H * a.nsplit <= kMaxFlags ? (uint32_t *)(p + kCounterBytes) : nullptr;
+  a.recs = nullptr;  // the GQA-4 grid launcher opts in (records_of)
   p += kCounterRegion;
   const size_t ml = (size_t)a.B * a.nq * a.nsplit * 2 * sizeof(float);
   a.part_ml = (float *)p;
   p += round256(ml);
   a.part_acc = (float *)p;
+}
+
+// The fold-record region of a carved workspace.
+inline uint32_t *records_of(void *ws) {
+  return (uint32_t *)((char *)ws + kCounterBytes + kFlagBytes);
 }
 
 // Common launch preparation: split plan and workspace.  chunk_heads = q heads
@@ -456,7 +472,7 @@ inline int setup_workspace(DecodeArgs &a, void *workspace, size_t ws_bytes) {
     carve_workspace(a, workspace);
   } else {
     a.part_ml = a.part_acc = nullptr;
-    a.counters = a.flags = nullptr;
+    a.counters = a.flags = a.recs = nullptr;
   }
   return CQ_OK;
 }

@@ -159,6 +159,110 @@ __device__ __forceinline__ void merge_partials_g4(const DecodeArgs &a, __amdgpu_
   }
 }
 
+// ---------------------------------------------------------------------------
+// Fold records (grid plan, when its workgroups are one resident generation):
+// every live split stores its partial as records of 12 words per (head, 8
+// dims) unit (m, l, 2 unused, 8 outputs), each word the bit pattern + 1 (a
+// zero word is "not written"; only the NaN pattern 0xffffffff maps to zero,
+// and a record holding it is folded when the poll bound runs out).  Split f
+// then folds the units u = f, f + live, f + 2 live, ...: each record is read
+// by exactly one folder, which polls it until all ten words are non-zero,
+// folds and writes the outputs, and stores zeros over it.  Data and readiness
+// arrive in one round trip; no flag, no counter, no acknowledgement wait.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ uint4 load_rec4(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  const i4_t v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, kPolicyDevice);
+  return uint4{(uint32_t)v[0], (uint32_t)v[1], (uint32_t)v[2], (uint32_t)v[3]};
+}
+__device__ __forceinline__ void store_rec1(__amdgpu_buffer_rsrc_t r, uint32_t off, float v) {
+  __builtin_amdgcn_raw_buffer_store_b32((int)(__float_as_uint(v) + 1u), r, (int)off, 0, kPolicyDevice);
+}
+__device__ __forceinline__ float rec_value(uint32_t w) { return __uint_as_float(w - 1u); }
+
+// max / sum over aligned groups of 2^lg lanes (lg <= 6, wave-uniform)
+__device__ __forceinline__ float group_max(float v, int lg) {
+  if (lg > 0) v = fmaxf(v, dpp_f<kDppQuadXor1>(v));
+  if (lg > 1) v = fmaxf(v, dpp_f<kDppQuadXor2>(v));
+  if (lg > 2) v = fmaxf(v, dpp_f<kDppRowHalfMirror>(v));
+  if (lg > 3) v = fmaxf(v, dpp_f<kDppRowMirror>(v));
+  if (lg > 4) v = fmaxf(v, __shfl_xor(v, 16, 64));
+  if (lg > 5) v = fmaxf(v, __shfl_xor(v, 32, 64));
+  return v;
+}
+__device__ __forceinline__ float group_sum(float v, int lg) {
+  if (lg > 0) v += dpp_f<kDppQuadXor1>(v);
+  if (lg > 1) v += dpp_f<kDppQuadXor2>(v);
+  if (lg > 2) v += dpp_f<kDppRowHalfMirror>(v);
+  if (lg > 3) v += dpp_f<kDppRowMirror>(v);
+  if (lg > 4) v += __shfl_xor(v, 16, 64);
+  if (lg > 5) v += __shfl_xor(v, 32, 64);
+  return v;
+}
+
+constexpr int kRecPollRounds = 1 << 20;
+
+// Wave 0 of split f's workgroup folds its units; lane = (unit k of the pass,
+// split s), 2^lg >= live lanes per unit.
+__device__ __forceinline__ void fold_records_g4(const DecodeArgs &a, int b, int h, int gn, int f,
+                                                int live) {
+  if (threadIdx.x >= 64) return;
+  const int lane = threadIdx.x;
+  const int lg = live > 1 ? 32 - __builtin_clz((uint32_t)(live - 1)) : 0;
+  const int s = lane & ((1 << lg) - 1), k = lane >> lg;
+  const int per_pass = 64 >> lg;
+  const int nunits = kD / 8 * gn;
+  const __amdgpu_buffer_rsrc_t rr = make_rsrc(a.recs, (uint32_t)kRecBytes);
+  const int64_t col = (int64_t)b * a.H + h;
+  for (int j0 = 0; f + live * j0 < nunits; j0 += per_pass) {
+    const int u = f + live * (j0 + k);
+    const bool valid = s < live && u < nunits;
+    const uint32_t off =
+        (uint32_t)(((col * a.nsplit + s) * kRecUnits + (valid ? u : 0)) * (kRecWords * 4));
+    uint4 hv = uint4{0u, 0u, 0u, 0u}, o0 = hv, o1 = hv;
+    for (int round = 0; round < kRecPollRounds; ++round) {
+      if (valid) {
+        hv = load_rec4(rr, off);
+        o0 = load_rec4(rr, off + 16u);
+        o1 = load_rec4(rr, off + 32u);
+      }
+      const bool ok = !valid || (hv.x && hv.y && o0.x && o0.y && o0.z && o0.w && o1.x && o1.y &&
+                                 o1.z && o1.w);
+      if (__all(ok)) break;
+      __builtin_amdgcn_s_sleep(1);
+    }
+    const float m = valid ? rec_value(hv.x) : -INFINITY;
+    const float M = group_max(m, lg);
+    const float w = (m == -INFINITY) ? 0.f : fast_exp2(m - M);
+    const float L = group_sum(valid ? w * rec_value(hv.y) : 0.f, lg);
+    const uint32_t ow[8] = {o0.x, o0.y, o0.z, o0.w, o1.x, o1.y, o1.z, o1.w};
+    float o[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[e] = group_sum(valid ? w * rec_value(ow[e]) : 0.f, lg);
+    if (valid) {
+      const i4_t z = i4_t{0, 0, 0, 0};
+      __builtin_amdgcn_raw_buffer_store_b128(z, rr, (int)off, 0, kPolicyDevice);
+      __builtin_amdgcn_raw_buffer_store_b128(z, rr, (int)off + 16, 0, kPolicyDevice);
+      __builtin_amdgcn_raw_buffer_store_b128(z, rr, (int)off + 32, 0, kPolicyDevice);
+      if (s == 0) {
+        const float inv = L > 0.f ? 1.f / L : 0.f;
+        const int64_t oi = ((int64_t)b * a.nq + h * a.G + (u >> 4)) * kD + 8 * (u & 15);
+        if (a.out_dtype == CQ_F16) {
+          h2v_t hp[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            hp[e] = h2v_t{(_Float16)(o[2 * e] * inv), (_Float16)(o[2 * e + 1] * inv)};
+          *(uint4 *)((uint16_t *)a.out + oi) =
+              uint4{__builtin_bit_cast(uint32_t, hp[0]), __builtin_bit_cast(uint32_t, hp[1]),
+                    __builtin_bit_cast(uint32_t, hp[2]), __builtin_bit_cast(uint32_t, hp[3])};
+        } else {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) store_any(a.out_dtype, a.out, oi + e, o[e] * inv);
+        }
+      }
+    }
+  }
+}
+
 // Slot 0's wait for the split-ready flags fl[1 .. live-1]: wave 0 polls them
 // with device-scope loads (one per lane per round) until every flag is set,
 // sleeping between rounds; the other waves wait at the barrier.  The other
@@ -214,7 +318,7 @@ __device__ __forceinline__ void merge_finish_g4(const DecodeArgs &a, G4Merge &M,
   const int64_t bq0 = (int64_t)b * a.nq + h * a.G;
   const bool single = live == kGridLive ? a.nsplit == 1 : live == 1;
   __amdgpu_buffer_rsrc_t racc, rml;
-  if (!single) partial_rsrcs(a, racc, rml);
+  if (!single && !a.recs) partial_rsrcs(a, racc, rml);
   if (hh < gn) {
     const float4 m0 = *(const float4 *)&M.m[hh][0], m1 = *(const float4 *)&M.m[hh][4];
     const float4 l0 = *(const float4 *)&M.l[hh][0], l1 = *(const float4 *)&M.l[hh][4];
@@ -232,6 +336,15 @@ __device__ __forceinline__ void merge_finish_g4(const DecodeArgs &a, G4Merge &M,
     }
     if (single) {
       store_any(a.out_dtype, a.out, (bq0 + hh) * kD + d, L > 0.f ? O / L : 0.f);
+    } else if (a.recs) {
+      const __amdgpu_buffer_rsrc_t rr = make_rsrc(a.recs, (uint32_t)kRecBytes);
+      const uint32_t rec = (uint32_t)(((((int64_t)b * a.H + h) * a.nsplit + slot) * kRecUnits +
+                                       hh * (kD / 8) + (d >> 3)) * (kRecWords * 4));
+      store_rec1(rr, rec + 16u + 4u * (uint32_t)(d & 7), O);
+      if ((d & 7) == 0) {
+        store_rec1(rr, rec, mm);
+        store_rec1(rr, rec + 4u, L);
+      }
     } else {
       const uint32_t row = (uint32_t)((bq0 + hh) * a.nsplit + slot);
       store_dev1(racc, (row * (uint32_t)kD + (uint32_t)d) * 4u, O);
@@ -240,6 +353,10 @@ __device__ __forceinline__ void merge_finish_g4(const DecodeArgs &a, G4Merge &M,
   }
   if (single) return;
   if (live == kGridLive) live = grid_live(a, seq_len_of(a, b));
+  if (a.recs) {
+    fold_records_g4(a, b, h, gn, slot, live);
+    return;
+  }
   if (a.flags) {
     // Split-ready flags: every split but slot 0 publishes its partial and
     // sets its flag; slot 0 waits for the flags and folds.  No atomics, so
@@ -299,8 +416,9 @@ struct G4Buf {
 // where it is as balanced as the partition below).  kBalanced = true: the
 // balanced partition of the batch's units (cq_plan.h), one or more segments
 // per workgroup.
-template <bool kBalanced>
+template <bool kBalanced, bool kOneChunk = false>
 __global__ __launch_bounds__(kThreadsMfma) void decode_g4_kernel(DecodeArgs a) {
+  static_assert(!(kBalanced && kOneChunk), "one-chunk splits are a grid plan");
   __shared__ G4Lds lds;
   __shared__ int32_t s_units[kBalanced ? kMaxTableSeqs + 1 : 1];
   // Balanced plan: workgroup p of the column takes units [floor(pU/P),
@@ -691,8 +809,11 @@ __global__ __launch_bounds__(kThreadsMfma) void decode_g4_kernel(DecodeArgs a) {
     };
 
     // Software pipeline: the next chunk's loads are issued before the current
-    // chunk is computed (two register buffers, unrolled by two).
-    if (has_work) {
+    // chunk is computed (two register buffers, unrolled by two).  Splits of at
+    // most one chunk per wave (kOneChunk) have nothing to pipeline.
+    if constexpr (kOneChunk) {
+      if (has_work) compute(bufA, 0);
+    } else if (has_work) {
       for (;;) {
         stage((int)(c0l + kWaves * kChunk), bufB);
         compute(bufA, 0);
@@ -781,12 +902,20 @@ int launch_decode_g4(DecodeArgs &a, void *workspace, size_t ws_bytes, hipStream_
   }
   int st = setup_workspace(a, workspace, ws_bytes);
   if (st) return st;
+  // Fold records: every split waits for the others, so the grid must be one
+  // resident generation; a folder's lanes hold up to 64 splits.
+  const int64_t slots = (int64_t)a.B * a.H * a.nsplit;
+  if (!balanced && a.nsplit > 1 && a.nsplit <= 64 && slots <= kMaxRecSplits && slots <= resident)
+    a.recs = records_of(workspace);
   if (balanced) {
     const dim3 grid((unsigned)P, (unsigned)a.H, 1u);
     decode_g4_kernel<true><<<grid, dim3(kThreadsMfma), 0, stream>>>(a);
   } else {
     const dim3 grid((unsigned)a.nsplit, (unsigned)a.H, (unsigned)a.B);
-    decode_g4_kernel<false><<<grid, dim3(kThreadsMfma), 0, stream>>>(a);
+    if (a.split_len <= (int64_t)kWaves * kChunk)
+      decode_g4_kernel<false, true><<<grid, dim3(kThreadsMfma), 0, stream>>>(a);
+    else
+      decode_g4_kernel<false><<<grid, dim3(kThreadsMfma), 0, stream>>>(a);
   }
   return hipGetLastError() == hipSuccess ? CQ_OK : CQ_ERR_LAUNCH;
 }

@@ -117,11 +117,12 @@ int cq_reconstruct(const cq_cache_desc *cache, int32_t component,
                    int64_t seq_len, uint16_t *out, cq_stream_t stream);
 
 /* Bytes of workspace cq_decode_attn needs for this shape.  The workspace
- * must be zero-filled once before its first use.  Its first 256 KiB hold the
- * split counters (one per sequence x kv head x q-head chunk, at most 16384)
- * and split-ready flags, which every call returns to zero, so one workspace
- * can be reused — also by calls of other shapes — without clearing.  Calls that share a workspace
- * must be ordered on one stream.  The workspace must be 256-byte aligned. */
+ * must be zero-filled once before its first use.  Its first 1.75 MiB hold the
+ * split counters (one per sequence x kv head x q-head chunk, at most 16384),
+ * split-ready flags and split fold records, which every call returns to
+ * zero, so one workspace can be reused — also by calls of other shapes and
+ * by cq_prefill_attn — without clearing.  Calls that share a workspace must
+ * be ordered on one stream.  The workspace must be 256-byte aligned. */
 size_t cq_decode_workspace_size(int32_t batch, int32_t n_kv_heads,
                                 int32_t n_q_heads, int32_t head_dim,
                                 int64_t max_seq_len);
