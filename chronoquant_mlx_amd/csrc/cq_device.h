@@ -112,6 +112,14 @@ __device__ __forceinline__ uint32_t dpp_u(uint32_t v) {
                                                 0xf, false);
 }
 
+// max(a, b) of non-NaN values as one v_max_f32: fmaxf in IEEE mode first
+// canonicalises every operand the compiler cannot prove canonical (values
+// moved across lanes, converted halves), one extra VALU each.
+__device__ __forceinline__ float max_nn(float a, float b) {
+  float r;
+  asm("v_max_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
+  return r;
+}
 __device__ __forceinline__ float wave_max(float v) {
   v = fmaxf(v, dpp_f<kDppQuadXor1>(v));
   v = fmaxf(v, dpp_f<kDppQuadXor2>(v));
@@ -149,8 +157,8 @@ __device__ __forceinline__ float row16_sum(float v) {
 }
 // Max over the 4 lanes of a row congruent to this lane mod 4.
 __device__ __forceinline__ float row16_mod4_max(float v) {
-  v = fmaxf(v, dpp_f<kDppRowRor4>(v));
-  return fmaxf(v, dpp_f<kDppRowRor8>(v));
+  v = max_nn(v, dpp_f<kDppRowRor4>(v));
+  return max_nn(v, dpp_f<kDppRowRor8>(v));
 }
 __device__ __forceinline__ float row16_mod4_sum(float v) {
   v += dpp_f<kDppRowRor4>(v);
@@ -163,11 +171,11 @@ __device__ __forceinline__ float row16_mod4_sum(float v) {
 // that order, so both lanes of a pair compute the same bits.
 __device__ __forceinline__ float xor16_max(float v) {
   const auto q = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-  return fmaxf(__uint_as_float(q[0]), __uint_as_float(q[1]));
+  return max_nn(__uint_as_float(q[0]), __uint_as_float(q[1]));
 }
 __device__ __forceinline__ float xor32_max(float v) {
   const auto q = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-  return fmaxf(__uint_as_float(q[0]), __uint_as_float(q[1]));
+  return max_nn(__uint_as_float(q[0]), __uint_as_float(q[1]));
 }
 __device__ __forceinline__ float xor16_sum(float v) {
   const auto q = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);

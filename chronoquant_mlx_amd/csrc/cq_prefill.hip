@@ -87,6 +87,13 @@ __device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
 }
 
 __device__ __forceinline__ h2_t as_h2(uint32_t u) { return __builtin_bit_cast(h2_t, u); }
+// Packed fp16 max of non-NaN pairs, without the canonicalising moves the
+// compiler puts around v_pk_max_f16 in IEEE mode.
+__device__ __forceinline__ h2_t pk_max_nn(h2_t a, h2_t b) {
+  h2_t r;
+  asm("v_pk_max_f16 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
+  return r;
+}
 __device__ __forceinline__ uint32_t as_u(h2_t h) { return __builtin_bit_cast(uint32_t, h); }
 __device__ __forceinline__ h8_t h8_of(uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
   const h2_t x = as_h2(a), y = as_h2(b), z = as_h2(c), w = as_h2(d);
@@ -136,9 +143,11 @@ __device__ __forceinline__ uint4 rebuild8(uint32_t cw, uint4 a, h2_t s2, uint32_
 // pairs on rows 8..15 of every 16.
 __device__ __forceinline__ int vt_col(int row, int g) { return 4 * (g ^ ((row >> 3) & 1)); }
 
+// Two block buffers: block kb + 1 is rebuilt into one while block kb's
+// products read the other, so each block needs one barrier.
 struct alignas(16) PrefillLds {
-  uint16_t k[kKeys][kKStride];  // K block, [key][dim (grouped order)]
-  uint16_t v[kD][kVStride];     // V block transposed, [dim (grouped order)][key]
+  uint16_t k[2][kKeys][kKStride];  // K block, [key][dim (grouped order)]
+  uint16_t v[2][kD][kVStride];     // V block transposed, [dim (grouped order)][key]
 };
 
 // Split epilogue: this workgroup's rows' (m, l, o) go to the workspace with
@@ -380,16 +389,12 @@ void prefill_mfma_kernel(PrefillArgs a) {
     }
   };
 
-  // The staging registers are free once a block is rebuilt in LDS: the next
-  // block's loads go out right after that barrier, so their latency overlaps
-  // this block's products and softmax instead of stalling the next rebuild.
-  if (kb_lo < kb_hi) load_block(kb_lo * kKeys);
-  for (int kb = kb_lo; kb < kb_hi; ++kb) {
-    const int k0 = kb * kKeys;
-    // ---- 1. rebuild the K (waves 0-7) or V (waves 8-15) block in LDS -----------
+  // ---- 1. rebuild the staged block: K (waves 0-7) or V (waves 8-15) into
+  // LDS buffer `buf` --------------------------------------------------------------
+  auto rebuild = [&](int buf) {
     if (kside) {
       const h2_t s2 = as_h2(r_s[0] * 0x10001u);
-      uint4 *dst = (uint4 *)&lds.k[kkey][16 * ke];
+      uint4 *dst = (uint4 *)&lds.k[buf][kkey][16 * ke];
 #pragma unroll
       for (int j = 0; j < 2; ++j) dst[j] = rebuild8(r_cw[j], r_an[j], s2, magic);
     } else {
@@ -404,27 +409,46 @@ void prefill_mfma_kernel(PrefillArgs a) {
         const uint32_t w0 = dw == 0 ? r[0].x : dw == 1 ? r[0].y : dw == 2 ? r[0].z : r[0].w;
         const uint32_t w1 = dw == 0 ? r[1].x : dw == 1 ? r[1].y : dw == 2 ? r[1].z : r[1].w;
         const int row = 8 * vw + i;
-        *(uint32_t *)&lds.v[row][vt_col(row, vkp >> 1) + 2 * (vkp & 1)] =
+        *(uint32_t *)&lds.v[buf][row][vt_col(row, vkp >> 1) + 2 * (vkp & 1)] =
             __builtin_amdgcn_perm(w1, w0, sel);
       }
     }
-    __syncthreads();
-    if (kb + 1 < kb_hi) load_block(k0 + kKeys);  // uniform
+  };
+
+  // Pipeline: while block kb's products read one LDS buffer, the waves
+  // rebuild block kb + 1 (staged in registers during block kb - 1) into the
+  // other and issue block kb + 2's loads; one barrier per block.
+  if (kb_lo < kb_hi) {  // uniform
+    load_block(kb_lo * kKeys);
+    rebuild(0);
+    if (kb_lo + 1 < kb_hi) load_block((kb_lo + 1) * kKeys);
+  }
+  __syncthreads();
+  for (int kb = kb_lo; kb < kb_hi; ++kb) {
+    const int k0 = kb * kKeys;
+    const int cur = (kb - kb_lo) & 1;
+    if (kb + 1 < kb_hi) {  // uniform
+      rebuild(cur ^ 1);
+      if (kb + 2 < kb_hi) load_block(k0 + 2 * kKeys);
+    }
 
     // ---- 2. S^T = K . Q^T: lane (col = row, kg) gets keys 16t + 4kg + r ---------
+    // Scores in natural units: the log2 scaling is folded into the
+    // exponent's fma below, and the row max is scaled once (scaling by
+    // log2 e > 0 keeps the max).  fp16 q: rounded to fp16 like the
+    // fallback's fp16 matmul and kept packed (s2, two per register): the max
+    // runs on the pairs and the exponent's fma reads an fp16 half directly.
+    // bf16 q: fp32 (sc).
     float sc[4][4];
+    h2_t s2[4][2];
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
       f4_t d = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int s = 0; s < 4; ++s) {
-        const uint4 kv = *(const uint4 *)&lds.k[16 * t + col][32 * s + 8 * kg];
+        const uint4 kv = *(const uint4 *)&lds.k[cur][16 * t + col][32 * s + 8 * kg];
         d = mfma32(__builtin_bit_cast(h8_t, kv), qf[s], d);
       }
-      // fp16 q: scores rounded to fp16 like the fallback's fp16 matmul (two
-      // per conversion).  sc stays in natural units: the log2 scaling is
-      // folded into the exponent's fma below, and the row max is scaled once
-      // (scaling by log2 e > 0 keeps the max).
 #pragma unroll
       for (int r = 0; r < 4; r += 2) {
         if (Bf16) {
@@ -432,9 +456,7 @@ void prefill_mfma_kernel(PrefillArgs a) {
           sc[t][r + 1] = d[r + 1];
         } else {
           typedef float f2_t __attribute__((ext_vector_type(2)));
-          const h2_t s16 = __builtin_convertvector(f2_t{d[r], d[r + 1]}, h2_t);
-          sc[t][r] = (float)s16.x;
-          sc[t][r + 1] = (float)s16.y;
+          s2[t][r >> 1] = __builtin_convertvector(f2_t{d[r], d[r + 1]}, h2_t);
         }
       }
     }
@@ -444,12 +466,25 @@ void prefill_mfma_kernel(PrefillArgs a) {
       for (int t = 0; t < 4; ++t)
 #pragma unroll
         for (int r = 0; r < 4; ++r)
-          if (k0 + 16 * t + 4 * kg + r > lim) sc[t][r] = -INFINITY;
+          if (k0 + 16 * t + 4 * kg + r > lim) {
+            if (Bf16)
+              sc[t][r] = -INFINITY;
+            else
+              s2[t][r >> 1][r & 1] = (_Float16)-INFINITY;
+          }
     }
-    float mx = -INFINITY;
+    float mx;
+    if (Bf16) {
+      mx = -INFINITY;
 #pragma unroll
-    for (int t = 0; t < 4; ++t)
-      mx = fmaxf(mx, fmaxf(fmaxf(sc[t][0], sc[t][1]), fmaxf(sc[t][2], sc[t][3])));
+      for (int t = 0; t < 4; ++t)
+        mx = fmaxf(mx, fmaxf(fmaxf(sc[t][0], sc[t][1]), fmaxf(sc[t][2], sc[t][3])));
+    } else {
+      h2_t m2 = pk_max_nn(s2[0][0], s2[0][1]);
+#pragma unroll
+      for (int t = 1; t < 4; ++t) m2 = pk_max_nn(m2, pk_max_nn(s2[t][0], s2[t][1]));
+      mx = max_nn((float)m2.x, (float)m2.y);
+    }
     // ---- 3. online softmax (row max over the 4 lane groups of the column) -------
     mx = xor32_max(xor16_max(mx)) * kLog2e;  // log2 units, as m_run
     if (__any(mx > m_run + kTau)) {
@@ -473,8 +508,10 @@ void prefill_mfma_kernel(PrefillArgs a) {
       // values P.V uses) in fp32, two per v_dot2_f32_f16
 #pragma unroll
       for (int u = 0; u < 2; ++u) {
-        pp[t][u] = h2_t{(_Float16)fast_exp2(__builtin_fmaf(sc[t][2 * u], kLog2e, -mref)),
-                        (_Float16)fast_exp2(__builtin_fmaf(sc[t][2 * u + 1], kLog2e, -mref))};
+        const float x0 = Bf16 ? sc[t][2 * u] : (float)s2[t][u].x;
+        const float x1 = Bf16 ? sc[t][2 * u + 1] : (float)s2[t][u].y;
+        pp[t][u] = h2_t{(_Float16)fast_exp2(__builtin_fmaf(x0, kLog2e, -mref)),
+                        (_Float16)fast_exp2(__builtin_fmaf(x1, kLog2e, -mref))};
         l_run = __builtin_amdgcn_fdot2(pp[t][u], ones, l_run, false);
       }
     }
@@ -486,12 +523,12 @@ void prefill_mfma_kernel(PrefillArgs a) {
                             as_u(pp[2 * P + 1][1]));
 #pragma unroll
       for (int dt = 0; dt < 8; ++dt) {
-        const uint2 v0 = *(const uint2 *)&lds.v[16 * dt + col][vt_col(col, 8 * P + kg)];
-        const uint2 v1 = *(const uint2 *)&lds.v[16 * dt + col][vt_col(col, 8 * P + 4 + kg)];
+        const uint2 v0 = *(const uint2 *)&lds.v[cur][16 * dt + col][vt_col(col, 8 * P + kg)];
+        const uint2 v1 = *(const uint2 *)&lds.v[cur][16 * dt + col][vt_col(col, 8 * P + 4 + kg)];
         acc[dt] = mfma32(ap, h8_of(v0.x, v0.y, v1.x, v1.y), acc[dt]);
       }
     }
-    __syncthreads();  // the next block overwrites LDS
+    __syncthreads();  // buffer cur is rebuilt next iteration
   }
 
   // ---- output: lane (col = grouped dim 16dt + col, kg) holds rows 4kg + r -------
