@@ -155,6 +155,34 @@ def kernel_source_hash():
     return h.hexdigest()[:16]
 
 
+PREFILL_COUNTERS_FILE = os.path.join(ROOT, "profiles", "prefill_c4_chunk_counters.txt")
+
+
+def prefill_source_hash():
+    import hashlib
+    h = hashlib.sha256()
+    for f in ("cq_prefill.hip", "cq_decode_common.h", "cq_plan.h", "cq_device.h"):
+        with open(os.path.join(ROOT, "chronoquant_mlx_amd", "csrc", f), "rb") as fh:
+            h.update(fh.read())
+    return h.hexdigest()[:16]
+
+
+def measured_prefill_mfma_busy():
+    """MFMA busy fraction of the prefill kernel (SQ_VALU_MFMA_BUSY_CYCLES per
+    SIMD over the dispatch's cycles) from the committed rocprofv3 --pmc
+    summary, if it was measured on the current kernel source."""
+    try:
+        with open(PREFILL_COUNTERS_FILE) as fh:
+            kv = dict(line.split("=", 1) for line in fh.read().splitlines() if "=" in line
+                      and not line.startswith((" ", "#", "rocprofv3")))
+    except OSError:
+        return None
+    kv = {a.strip(): b.strip() for a, b in kv.items()}
+    if kv.get("kernel_source_sha256_16") != prefill_source_hash():
+        return None
+    return float(kv["mfma_busy_frac"])
+
+
 def measured_traffic(workload):
     """HBM bytes per launch from the committed rocprofv3 --pmc summary, if it
     was measured on the current kernel source and this workload."""
@@ -374,7 +402,10 @@ def time_prefill(dev, stream, steps, T=8192, L=512):
            "us_per_call": round(ms * 1e3, 2), "TFLOPs": round(tf, 2),
            "frac_of_fp16_mfma_peak": round(tf / 2500.0, 4), "flops_per_call": flops,
            "reconstruct_fallback_us": round(ms_fb * 1e3, 2),
-           "speedup_vs_fallback": round(ms_fb / ms, 2)}
+           "speedup_vs_fallback": round(ms_fb / ms, 2),
+           # from profiles/prefill_c4_chunk_counters.txt (null when the kernel
+           # source changed since it was measured)
+           "mfma_busy_frac": measured_prefill_mfma_busy()}
     del cache
     torch.cuda.empty_cache()
     return res
