@@ -266,6 +266,35 @@ def test_output_dtypes_and_fp32_queries():
     assert_close(outq[0], exact)
 
 
+@pytest.mark.parametrize("out_dtype", ["f16", "bf16", "f32"])
+def test_split_fold_outputs_and_short_bound_lengths(out_dtype):
+    # The split fold of the grid plan (several splits of one sequence fold
+    # their partials into the output) with every output dtype, and with a
+    # device length shorter than the cache, so that fewer splits than the
+    # plan's hold tokens: T=3000 gives 6 splits of 512 tokens, length 1300
+    # leaves 3 of them live.
+    from chronoquant_mlx_amd.kernels import chronoquant_sdpa_kernel
+    dt = {"f16": torch.float16, "bf16": torch.bfloat16, "f32": torch.float32}[out_dtype]
+    rng = np.random.default_rng(31 + len(out_dtype))
+    B, H, T, D, G = 1, 8, 3000, 128, 4
+    k = np.cumsum(rng.standard_normal((B, H, T, D)) * 0.1, axis=2).astype(np.float16)
+    v = np.cumsum(rng.standard_normal((B, H, T, D)) * 0.1, axis=2).astype(np.float16)
+    q = rng.standard_normal((B, G * H, D)).astype(np.float16)
+    params = dict(stride_k=32, stride_v=8)
+    cache = build_gpu_cache(k, v, **params)
+    scale = D ** -0.5
+    # bf16 output: one more rounding of |o| < 1 at 2^-9 relative
+    atol, rtol = {"f16": (5e-4, 2e-3), "bf16": (2e-3, 8e-3), "f32": (5e-5, 2.5e-4)}[out_dtype]
+    for L in (T, 1300):
+        lens = None if L == T else torch.tensor([L], dtype=torch.int32, device="cuda")
+        out = chronoquant_sdpa_kernel(to_gpu(q), cache, scale, out_dtype=dt,
+                                      seq_lens=lens).float().cpu().numpy()
+        ck, cv = build_oracle(k[0][:, :L], v[0][:, :L], **params)
+        assert_close(out[0], oracle_fallback(ck, cv, q[0], scale), what=f"{out_dtype} L={L}")
+        assert_close(out[0], O.sdpa_fused(q[0], ck, cv, scale), atol, rtol,
+                     what=f"{out_dtype} L={L} vs fused semantics")
+
+
 def test_fp16_baseline_matches_exact():
     from chronoquant_mlx_amd import _lib
     rng = np.random.default_rng(8)
