@@ -39,9 +39,27 @@ namespace {
 
 constexpr int kG4 = 4;  // q heads per kv head this kernel serves
 
+// Code rows of the chunk being computed, by token (row kChunk: junk), rows
+// padded to 20 words so that 16 consecutive rows start on distinct 4-bank
+// groups: the pipelined instance loads a chunk's P-frame rows as contiguous
+// blocks and scatters them here to their tokens.
+constexpr int kRowWords = 20;
+struct alignas(16) G4Rows {
+  uint32_t k[kChunk + 1][kRowWords];
+  uint32_t v[kChunk + 1][kRowWords];
+};
+
+template <bool kContig>
+struct G4WaveRows {};
+template <>
+struct G4WaveRows<true> {
+  G4Rows rows;
+};
+
 // Per-wave LDS.  s16 is double-buffered (the chunk being computed and the one
 // whose loads are in flight).
-struct alignas(16) G4WaveScratch {
+template <bool kContig>
+struct alignas(16) G4WaveScratch : G4WaveRows<kContig> {
   int slot_v[kChunk];            // V P-frame slot per token (-1: I-frame / padding)
   uint32_t s16[2][kChunk];       // fp16 K scale | fp16 V scale << 16 (0: none)
   float qa[16][kG4];             // log2e * q'.anchor_k - mref by (local anchor, head)
@@ -61,9 +79,10 @@ struct alignas(16) G4GroupScratch {
   float s8[kG4];  // 8 * sum_d q'_d per head
 };
 
+template <bool kContig>
 struct G4Stage {
   G4GroupScratch g;
-  G4WaveScratch w[kWaves];
+  G4WaveScratch<kContig> w[kWaves];
 };
 
 // The workgroup merge: every wave's unnormalised output tile and its (m, l)
@@ -76,8 +95,9 @@ struct alignas(16) G4Merge {
 
 // The merge area is separate from the staging area, so a wave writes its
 // tile as soon as its own chunks are done.
+template <bool kContig>
 struct G4Lds {
-  G4Stage s;
+  G4Stage<kContig> s;
   G4Merge mg;
 };
 
@@ -400,7 +420,10 @@ __device__ __forceinline__ h8_t anchor_pair(uint4 u, uint4 v, bool odd) {
                __builtin_amdgcn_perm(v.z, v.x, sel), __builtin_amdgcn_perm(v.w, v.y, sel));
 }
 
-// The registers one chunk's loads land in.
+// The registers one chunk's loads land in.  kr and vw first hold the chunk's
+// contiguous K and V code blocks (16 bytes of slot row base + 16q + lane / 4,
+// quarter lane % 4, per register), then, once scattered through LDS, the
+// layouts the products read:
 struct G4Buf {
   uint4 kr[4];        // K code row of this lane's token (words 4q .. 4q+3 in kr[q])
   uint4 ka[4];        // K anchor row gk_base + col, dims 32kg + 8kb .. +7
@@ -419,7 +442,11 @@ struct G4Buf {
 template <bool kBalanced, bool kOneChunk = false>
 __global__ __launch_bounds__(kThreadsMfma) void decode_g4_kernel(DecodeArgs a) {
   static_assert(!(kBalanced && kOneChunk), "one-chunk splits are a grid plan");
-  __shared__ G4Lds lds;
+  // Code loads: contiguous blocks scattered through LDS (the pipelined
+  // instance, where they are off the critical path), or each lane's own
+  // token rows (one-chunk splits and the balanced plan).
+  constexpr bool kContig = !kBalanced && !kOneChunk;
+  __shared__ G4Lds<kContig> lds;
   __shared__ int32_t s_units[kBalanced ? kMaxTableSeqs + 1 : 1];
   // Balanced plan: workgroup p of the column takes units [floor(pU/P),
   // floor((p+1)U/P)) of the batch's units laid end to end, one segment per
@@ -516,12 +543,37 @@ __global__ __launch_bounds__(kThreadsMfma) void decode_g4_kernel(DecodeArgs a) {
     const __amdgpu_buffer_rsrc_t r_scv = make_rsrc(a.sc[1] + bh * a.cap_pf[1], (uint32_t)(a.cap_pf[1] * 2));
 
     G4GroupScratch &Gs = lds.s.g;
-    G4WaveScratch &W = lds.s.w[wave];
+    G4WaveScratch<kContig> &W = lds.s.w[wave];
 
     // Stage the chunk at c0 into cb: the token phase (lane = token c0 + lane:
-    // scales, own K code row, V slot to LDS), then the K anchor rows and the V
-    // code words.  A chunk past the end (nt = 0) gets offsets past every buffer,
-    // so its loads return zeros without traffic; so do I-frame and padding slots.
+    // scales; per-token loads: own K code row, V slot to LDS), the code blocks
+    // (contiguous loads), then the K anchor rows and (per-token loads) the V
+    // code words.  A chunk past the end (nt = 0) gets offsets past every
+    // buffer, so its loads return zeros without traffic; so do I-frame and
+    // padding slots.
+    // Scatter targets (LDS words) of this lane's pieces of the contiguous code
+    // blocks: piece j holds slot row s = 16j + lane / 4 (relative to base),
+    // quarter lane % 4.  A computed chunk starts at c0 = 0 mod 64 (segments
+    // and splits start at multiples of 512), so the P-frame token of row s
+    // depends on s alone: for strides below 64 (c0 an I-frame) t = s +
+    // (s - 1) / (stride - 1), s >= 1; for larger strides t = s.  Rows of other
+    // tokens go to the junk row.  Rows of I-frame and padding tokens keep
+    // whatever they held: their scales are 0, so any finite nibbles there
+    // (every bit pattern is one) contribute 0.
+    auto scatter_word = [&](int j, int ls) {
+      const int sr = 16 * j + (lane >> 2);
+      int t = sr;
+      if (ls < 6) t = sr == 0 ? kChunk : sr + (sr - 1) / ((1 << ls) - 1);
+      return min(t, kChunk) * kRowWords + 4 * (lane & 3);
+    };
+    int wk[4], wv[4];
+    if constexpr (kContig) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        wk[j] = scatter_word(j, lsk);
+        wv[j] = scatter_word(j, lsv);
+      }
+    }
     auto stage = [&](int c0, G4Buf &cb) {
       const int nt = (int)max((int64_t)0, min((int64_t)kChunk, t1 - c0));
       cb.c0 = c0;
@@ -538,28 +590,48 @@ __global__ __launch_bounds__(kThreadsMfma) void decode_g4_kernel(DecodeArgs a) {
         // slot -1 reads past the buffer: scale 0, codes 0
         cb.sk = bload16(r_sck, (uint32_t)slk * 2u);
         cb.sv = bload16(r_scv, (uint32_t)slv * 2u);
+        if constexpr (!kContig) {
 #pragma unroll
-        // the row's 4 quarters: each load touches every 64-byte row of the chunk
-        // once, so these stay cacheable for the next three (no nt policy)
-        for (int q = 0; q < 4; ++q) {
-          const i4_t v = __builtin_amdgcn_raw_buffer_load_b128(r_pkk, (int)((uint32_t)slk * 64u + 16u * q), 0, 0);
-          cb.kr[q] = uint4{(uint32_t)v[0], (uint32_t)v[1], (uint32_t)v[2], (uint32_t)v[3]};
+          // the row's 4 quarters: each load touches every 64-byte row of the chunk
+          // once, so these stay cacheable for the next three (no nt policy)
+          for (int q = 0; q < 4; ++q) {
+            const i4_t v = __builtin_amdgcn_raw_buffer_load_b128(r_pkk, (int)((uint32_t)slk * 64u + 16u * q), 0, 0);
+            cb.kr[q] = uint4{(uint32_t)v[0], (uint32_t)v[1], (uint32_t)v[2], (uint32_t)v[3]};
+          }
+          W.slot_v[lane] = slv;
         }
-        W.slot_v[lane] = slv;
       }
-      wave_lds_sync();
+      if constexpr (kContig) {
+        // The chunk's code rows as contiguous 1 KB blocks: slot rows base ..
+        // base + 63, base the slot token c0 would have (every P-frame row of
+        // the chunk lies in them; rows before slot 0 or past the buffer read 0)
+        const uint32_t bk = ((uint32_t)(c0 - gk_base - 1) * 64u + 16u * lane) | dead;
+        const uint32_t bv = ((uint32_t)(c0 - (c0 >> lsv) - 1) * 64u + 16u * lane) | dead;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) cb.kr[q] = bload128(r_pkk, bk + 1024u * q);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const uint4 w = bload128(r_pkv, bv + 1024u * i);
+          cb.vw[i][0] = w.x;
+          cb.vw[i][1] = w.y;
+          cb.vw[i][2] = w.z;
+          cb.vw[i][3] = w.w;
+        }
+      }
       {
         const uint32_t row = ((uint32_t)min(gk_base + col, gk_last) * 256u + 64u * kg) | dead;
 #pragma unroll
         for (int kb = 0; kb < 4; ++kb) cb.ka[kb] = bload128(r_kfk, row + 16u * kb);
       }
+      if constexpr (!kContig) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int4 sl4 = *(const int4 *)&W.slot_v[16 * i + 4 * kg];
-        cb.vw[i][0] = bload32(r_pkv, (uint32_t)sl4.x * 64u + 4u * col);
-        cb.vw[i][1] = bload32(r_pkv, (uint32_t)sl4.y * 64u + 4u * col);
-        cb.vw[i][2] = bload32(r_pkv, (uint32_t)sl4.z * 64u + 4u * col);
-        cb.vw[i][3] = bload32(r_pkv, (uint32_t)sl4.w * 64u + 4u * col);
+        for (int i = 0; i < 4; ++i) {
+          const int4 sl4 = *(const int4 *)&W.slot_v[16 * i + 4 * kg];
+          cb.vw[i][0] = bload32(r_pkv, (uint32_t)sl4.x * 64u + 4u * col);
+          cb.vw[i][1] = bload32(r_pkv, (uint32_t)sl4.y * 64u + 4u * col);
+          cb.vw[i][2] = bload32(r_pkv, (uint32_t)sl4.z * 64u + 4u * col);
+          cb.vw[i][3] = bload32(r_pkv, (uint32_t)sl4.w * 64u + 4u * col);
+        }
       }
     };
     // V anchor rows gv_base + 4kg + r of the chunk at c0, dims 8col .. 8col+7.
@@ -643,6 +715,22 @@ __global__ __launch_bounds__(kThreadsMfma) void decode_g4_kernel(DecodeArgs a) {
       const int c0 = cb.c0;
       const int gk_base = c0 >> lsk, gv_base = c0 >> lsv;
       W.s16[sl][lane] = cb.sk | (cb.sv << 16);
+      if constexpr (kContig) {
+        // code rows by token: K row of this lane's token, V word col of tokens
+        // 16i + 4kg + r
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          *(uint4 *)&W.rows.k[0][wk[j]] = cb.kr[j];
+          *(uint4 *)&W.rows.v[0][wv[j]] = uint4{cb.vw[j][0], cb.vw[j][1], cb.vw[j][2], cb.vw[j][3]};
+        }
+        wave_lds_sync();
+#pragma unroll
+        for (int q = 0; q < 4; ++q) cb.kr[q] = *(const uint4 *)&W.rows.k[lane][4 * q];
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) cb.vw[i][r] = W.rows.v[16 * i + 4 * kg + r][col];
+      }
       // ---- anchor table: log2e * q'.a - mref for anchors gk_base + 4kg + r ----------
       // (C[anchor][head col]; the lanes col < 4 are head col's score lanes of
       // block 0, whose m_run is head col's)
