@@ -317,7 +317,8 @@ def time_streaming(name, dev, stream, n_steps=256):
     gcfg = dataclasses.replace(cfg, T=cap)
     cache, kt, vt = build_cache_device(gcfg, dev, capacity=cap)
     # every sequence holds t_max tokens; sequence b continues at lens[b]
-    n_layers = replica_count(cache.nbytes, floor=1)
+    algo = int(np.mean([synth.algorithmic_decode_bytes(cfg, lens + s + 1) for s in range(n_steps)]))
+    n_layers = replica_count(algo, floor=1)  # by the bytes a decode reads
     caches = [cache] + [clone_cache(cache) for _ in range(n_layers - 1)]
     descs = [c._descriptor() for c in caches]
     L = _lib.load()
@@ -365,7 +366,6 @@ def time_streaming(name, dev, stream, n_steps=256):
         e1.record(stream)
     e1.synchronize()
     ms = e0.elapsed_time(e1) / (n_steps * n_layers)
-    algo = int(np.mean([synth.algorithmic_decode_bytes(cfg, lens + s + 1) for s in range(n_steps)]))
     gbs = algo / (ms * 1e-3) / 1e9
     log(f"[bench] {name}: {ms * 1e3:.2f} us/step (append + decode), {gbs:.0f} GB/s")
     res = {"workload": f"B={B} ragged T_b~U[{cfg.ragged_min},{cfg.T}] GQA {nq}q/{H}kv strides "
