@@ -137,6 +137,28 @@ def test_strides_not_powers_of_two(sk, sv):
         assert_tight(out[b], O.sdpa_fused(q[b], ck, cv, scale), what=f"b={b}")
 
 
+@pytest.mark.parametrize("sk,sv", [(4, 8), (8, 4), (16, 32), (32, 128), (128, 16), (64, 64)])
+def test_pipelined_plan_strides(sk, sv):
+    # Two sequences of 9000 tokens over 8 kv heads: the grid plan gives 9
+    # splits of 1024 tokens (two 64-token chunks per wave), so the pipelined
+    # instance runs, which loads a chunk's code rows as contiguous slot blocks
+    # and scatters them to their tokens.  Strides below, at and above the
+    # chunk, and a last split that ends inside a chunk (waves past the end).
+    rng = np.random.default_rng(sk * 1000 + sv)
+    B, H, T, D, G = 2, 8, 9000, 128, 4
+    k = np.cumsum(rng.standard_normal((B, H, T, D)) * 0.1, axis=2).astype(np.float16)
+    v = np.cumsum(rng.standard_normal((B, H, T, D)) * 0.1, axis=2).astype(np.float16)
+    q = rng.standard_normal((B, G * H, D)).astype(np.float16)
+    params = dict(stride_k=sk, stride_v=sv)
+    cache = build_gpu_cache(k, v, **params)
+    scale = D ** -0.5
+    out = decode_gpu(cache, q, scale)
+    for b in range(B):
+        ck, cv = build_oracle(k[b], v[b], **params)
+        assert_close(out[b], oracle_fallback(ck, cv, q[b], scale), what=f"b={b}")
+        assert_tight(out[b], O.sdpa_fused(q[b], ck, cv, scale), what=f"b={b}")
+
+
 def test_workspace_shared_across_shapes():
     # regression: calls with different split counts share the per-device
     # workspace; counters must stay valid between them
