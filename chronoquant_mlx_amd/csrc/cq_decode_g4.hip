@@ -553,10 +553,11 @@ __global__ __launch_bounds__(kThreadsMfma) void decode_g4_kernel(DecodeArgs a) {
     // padding slots.
     // Scatter targets (LDS words) of this lane's pieces of the contiguous code
     // blocks: piece j holds slot row s = 16j + lane / 4 (relative to base),
-    // quarter lane % 4.  A computed chunk starts at c0 = 0 mod 64 (segments
-    // and splits start at multiples of 512), so the P-frame token of row s
-    // depends on s alone: for strides below 64 (c0 an I-frame) t = s +
-    // (s - 1) / (stride - 1), s >= 1; for larger strides t = s.  Rows of other
+    // quarter lane % 4.  A computed chunk starts at c0 = 0 mod 64 (splits
+    // start at multiples of the split length, itself a multiple of 64), so
+    // the P-frame token of row s depends on s alone: for strides below 64
+    // (c0 an I-frame) t = s + (s - 1) / (stride - 1), s >= 1; for larger
+    // strides t = s.  Rows of other
     // tokens go to the junk row.  Rows of I-frame and padding tokens keep
     // whatever they held: their scales are 0, so any finite nibbles there
     // (every bit pattern is one) contribute 0.
