@@ -557,10 +557,9 @@ __global__ __launch_bounds__(kThreadsMfma) void decode_g4_kernel(DecodeArgs a) {
     // start at multiples of the split length, itself a multiple of 64), so
     // the P-frame token of row s depends on s alone: for strides below 64
     // (c0 an I-frame) t = s + (s - 1) / (stride - 1), s >= 1; for larger
-    // strides t = s.  Rows of other
-    // tokens go to the junk row.  Rows of I-frame and padding tokens keep
-    // whatever they held: their scales are 0, so any finite nibbles there
-    // (every bit pattern is one) contribute 0.
+    // strides t = s.  Rows of other tokens go to the junk row.  Rows of
+    // I-frame and padding tokens keep whatever they held: their scales are 0,
+    // so any finite nibbles there (every bit pattern is one) contribute 0.
     auto scatter_word = [&](int j, int ls) {
       const int sr = 16 * j + (lane >> 2);
       int t = sr;
