@@ -159,6 +159,26 @@ def test_pipelined_plan_strides(sk, sv):
         assert_tight(out[b], O.sdpa_fused(q[b], ck, cv, scale), what=f"b={b}")
 
 
+def test_pipelined_plan_single_split():
+    # 40 sequences x 8 kv heads fill the grid without splitting: one
+    # workgroup per (sequence, kv head) over 640 tokens, so the pipelined
+    # instance runs with two chunks on waves 0-1 and one on the others, and
+    # writes the output without a fold.
+    rng = np.random.default_rng(77)
+    B, H, T, D, G = 40, 8, 640, 128, 4
+    k = np.cumsum(rng.standard_normal((B, H, T, D)) * 0.1, axis=2).astype(np.float16)
+    v = np.cumsum(rng.standard_normal((B, H, T, D)) * 0.1, axis=2).astype(np.float16)
+    q = rng.standard_normal((B, G * H, D)).astype(np.float16)
+    params = dict(stride_k=64, stride_v=32)
+    cache = build_gpu_cache(k, v, **params)
+    scale = D ** -0.5
+    out = decode_gpu(cache, q, scale)
+    for b in (0, 17, 39):
+        ck, cv = build_oracle(k[b], v[b], **params)
+        assert_close(out[b], oracle_fallback(ck, cv, q[b], scale), what=f"b={b}")
+        assert_tight(out[b], O.sdpa_fused(q[b], ck, cv, scale), what=f"b={b}")
+
+
 def test_workspace_shared_across_shapes():
     # regression: calls with different split counts share the per-device
     # workspace; counters must stay valid between them
