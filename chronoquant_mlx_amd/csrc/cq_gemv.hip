@@ -60,6 +60,7 @@ __device__ __forceinline__ uint4 ld128(__amdgpu_buffer_rsrc_t r, uint32_t off) {
 //           SwiGLU gate, as cq_silu_mul computes it.
 enum GemvMode { kPlain = 0, kNorm = 1, kSilu = 2 };
 constexpr int kGemvMaxNormK = 8192;  // h cached in LDS (16 KB of 16-bit values)
+constexpr unsigned kGemvPairMaxGroups = 1024;  // workgroups up to which kNorm takes kPair
 
 struct GemvArgs {
   const uint16_t *w;
@@ -98,7 +99,12 @@ __device__ __forceinline__ float round_dt(float v) {
   return DT == CQ_BF16 ? bf2f(f2bf(v)) : h2f(f2h(v));
 }
 
-template <int DT, int Mode>
+// kPair: a wave takes its blocks two at a time, with both blocks' 16 row
+// loads in flight before its first wait.  It pays where the whole grid is
+// resident at once (a few workgroups per CU, as in the QKV projection):
+// there the rows in flight per wave bound the rate.  With more workgroups
+// than fit at once it is slower (fewer waves per SIMD at its register count).
+template <int DT, int Mode, bool kPair = false>
 __global__ __launch_bounds__(kGemvThreads) void gemv_kernel(GemvArgs a) {
   __shared__ float red[kGemvWaves][kGemvRows];
   __shared__ uint4 hs[Mode == kNorm ? kGemvMaxNormK / 8 : 1];
@@ -143,6 +149,61 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_kernel(GemvArgs a) {
   float acc[kGemvRows];
 #pragma unroll
   for (int r = 0; r < kGemvRows; ++r) acc[r] = 0.f;
+  if constexpr (kPair) {
+    // both blocks' operands first, then their 16 weight rows; the blocks
+    // are still summed in increasing order
+    for (int blk = wave; blk * kGemvBlk < k; blk += 2 * kGemvWaves) {
+      int e[2];
+      bool in[2];
+      uint4 op[2][2];  // kPlain: x; kNorm: the norm weight; kSilu: gate, up
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        e[u] = (blk + u * kGemvWaves) * kGemvBlk + 8 * lane;
+        in[u] = e[u] < k;
+        const uint32_t off = in[u] ? (uint32_t)e[u] * 2u : kDead;
+        if constexpr (Mode == kNorm) {
+          op[u][0] = ld128<0>(rn, off);
+        } else {
+          op[u][0] = ld128<0>(rx, off);
+          if constexpr (Mode == kSilu)
+            op[u][1] = ld128<0>(rx, in[u] ? (uint32_t)(k + e[u]) * 2u : kDead);
+        }
+      }
+      uint4 wv[2][kGemvRows];
+#pragma unroll
+      for (int u = 0; u < 2; ++u)
+#pragma unroll
+        for (int r = 0; r < kGemvRows; ++r)
+          wv[u][r] = ld128<kPolicyStreamGemv>(
+              rw, (in[u] && r < rows) ? ((uint32_t)r * (uint32_t)k + (uint32_t)e[u]) * 2u : kDead);
+      // (the scheduler would otherwise sink the second block's loads below
+      // the first block's products to save registers)
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        uint4 xv;
+        if constexpr (Mode == kPlain) {
+          xv = op[u][0];
+        } else if constexpr (Mode == kNorm) {
+          float h[8], g[8];
+          unpack8f<DT>(in[u] ? hs[e[u] >> 3] : uint4{0u, 0u, 0u, 0u}, h);
+          unpack8f<DT>(op[u][0], g);
+#pragma unroll
+          for (int i = 0; i < 8; ++i) h[i] = h[i] * inv * g[i];
+          xv = pack8f<DT>(h);
+        } else {
+          float g[8], up[8];
+          unpack8f<DT>(op[u][0], g);
+          unpack8f<DT>(op[u][1], up);
+#pragma unroll
+          for (int i = 0; i < 8; ++i) g[i] = round_dt<DT>(g[i] / (1.f + expf(-g[i]))) * up[i];
+          xv = pack8f<DT>(g);
+        }
+#pragma unroll
+        for (int r = 0; r < kGemvRows; ++r) acc[r] = dot8<DT>(wv[u][r], xv, acc[r]);
+      }
+    }
+  } else {
 #pragma unroll 2
   for (int blk = wave; blk * kGemvBlk < k; blk += kGemvWaves) {
     const int e = blk * kGemvBlk + 8 * lane;  // this lane's 8 elements of every row
@@ -173,6 +234,7 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_kernel(GemvArgs a) {
 #pragma unroll
     for (int r = 0; r < kGemvRows; ++r) acc[r] = dot8<DT>(wv[r], xv, acc[r]);
   }
+  }
 #pragma unroll
   for (int r = 0; r < kGemvRows; ++r) {
     const float sm = wave_sum(acc[r]);
@@ -190,7 +252,10 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_kernel(GemvArgs a) {
 template <int DT>
 void launch_gemv(const GemvArgs &a, int mode, dim3 grid, hipStream_t s) {
   const dim3 blk(kGemvThreads);
-  if (mode == kNorm) gemv_kernel<DT, kNorm><<<grid, blk, 0, s>>>(a);
+  // the paired form where the grid is resident at once (a few workgroups
+  // per CU on MI355X's 256 CUs): the QKV projection, not gate/up
+  if (mode == kNorm && grid.x <= kGemvPairMaxGroups) gemv_kernel<DT, kNorm, true><<<grid, blk, 0, s>>>(a);
+  else if (mode == kNorm) gemv_kernel<DT, kNorm><<<grid, blk, 0, s>>>(a);
   else if (mode == kSilu) gemv_kernel<DT, kSilu><<<grid, blk, 0, s>>>(a);
   else gemv_kernel<DT, kPlain><<<grid, blk, 0, s>>>(a);
 }
