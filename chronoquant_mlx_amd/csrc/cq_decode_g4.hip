@@ -486,7 +486,9 @@ __global__ __launch_bounds__(kThreadsMfma) void decode_g4_kernel(DecodeArgs a) {
     // kept live across the body)
     const int tid = kBalanced ? thread_id() : (int)threadIdx.x;
     __builtin_assume(tid >= 0 && tid < kThreadsMfma);
-    const int lane = tid & 63, wave = tid >> 6;
+    // (the wave index in a scalar register: the chunk loop's bounds derive
+    // from it, so its branches are uniform)
+    const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int col = lane & 15, kg = lane >> 4;
     const int hq = col & 3;   // score layout: head of this lane's column
     const int jb = col >> 2;  // score layout: token block of this lane's column
@@ -902,18 +904,25 @@ __global__ __launch_bounds__(kThreadsMfma) void decode_g4_kernel(DecodeArgs a) {
     if constexpr (kOneChunk) {
       if (has_work) compute(bufA, 0);
     } else if (has_work) {
-      for (;;) {
-        stage((int)(c0l + kWaves * kChunk), bufB);
+      // The wave's n >= 1 chunks c0l, c0l + kStep, ... below t1, in pairs and
+      // one last single chunk, so that the loop has one exit, at its end.  (An
+      // exit between the two halves joins the loop header with the first
+      // half's loads in flight, and the header then waits for all of them
+      // before it issues the next chunk's.)  The last pair's V anchor loads
+      // are dead (offsets past the buffer, no memory access).
+      constexpr int64_t kStep = (int64_t)kWaves * kChunk;
+      int n = __builtin_amdgcn_readfirstlane((int)((t1 - c0l + kStep - 1) / kStep));
+      for (; n > 1; n -= 2) {
+        stage((int)(c0l + kStep), bufB);
         compute(bufA, 0);
-        c0l += kWaves * kChunk;
-        if (c0l >= t1) break;
+        c0l += kStep;
         stage_va((int)c0l);
-        stage((int)(c0l + kWaves * kChunk), bufA);
+        stage((int)(c0l + kStep), bufA);
         compute(bufB, 1);
-        c0l += kWaves * kChunk;
-        if (c0l >= t1) break;
+        c0l += kStep;
         stage_va((int)c0l);
       }
+      if (n) compute(bufA, 0);
     }
 
     // ---- totals of head hq: its 16 lanes hold disjoint tokens ---------------------------
