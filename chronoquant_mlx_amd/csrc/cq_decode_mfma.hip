@@ -106,7 +106,9 @@ __global__ __launch_bounds__(kThreadsMfma) void decode_mfma_kernel(DecodeArgs a)
   for (int it = 0;; ++it) {
     const int tid = kBalanced ? thread_id() : (int)threadIdx.x;
     __builtin_assume(tid >= 0 && tid < kThreadsMfma);
-    const int lane = tid & 63, wave = tid >> 6;
+    // (the wave index in a scalar register: the chunk loop's bounds derive
+    // from it, so its branches are uniform)
+    const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int col = lane & 15;  // q head (operand column) / 16-dim output column
     const int kg = lane >> 4;   // K group of the MFMA operands
     const int j0 = chunk * kHeads;
@@ -423,26 +425,32 @@ __global__ __launch_bounds__(kThreadsMfma) void decode_mfma_kernel(DecodeArgs a)
     };
 
     // Software pipeline: the next chunk's loads are issued before the current
-    // chunk is computed (two register buffers, unrolled by two).
+    // chunk is computed (two register buffers, unrolled by two).  The wave's
+    // n >= 1 chunks c0l, c0l + kStep, ... below t1 run in pairs and one last
+    // single chunk, so that the loop has one exit, at its end (an exit between
+    // the two halves joins the loop header with the first half's loads in
+    // flight, and the header then waits for all of them).  The last pair's V
+    // anchor loads are dead (offsets past the buffer, no memory access).
     int64_t c0l = t0 + (int64_t)wave * kChunk;
     if (c0l < t1) {
+      constexpr int64_t kStep = (int64_t)kWaves * kChunk;
       ChunkBuf bufA, bufB;
       if constexpr (kBalanced) bufA = bufB = ChunkBuf{};
       stage((int)c0l, bufA, 0);
       stage_va((int)c0l);
       prep_q();
-      for (;;) {
-        stage((int)(c0l + kWaves * kChunk), bufB, 1);
+      int n = __builtin_amdgcn_readfirstlane((int)((t1 - c0l + kStep - 1) / kStep));
+      for (; n > 1; n -= 2) {
+        stage((int)(c0l + kStep), bufB, 1);
         compute(bufA, 0);
-        c0l += kWaves * kChunk;
-        if (c0l >= t1) break;
+        c0l += kStep;
         stage_va((int)c0l);
-        stage((int)(c0l + kWaves * kChunk), bufA, 0);
+        stage((int)(c0l + kStep), bufA, 0);
         compute(bufB, 1);
-        c0l += kWaves * kChunk;
-        if (c0l >= t1) break;
+        c0l += kStep;
         stage_va((int)c0l);
       }
+      if (n) compute(bufA, 0);
     }
 
     // ---- totals: the 4 lane groups of a column hold disjoint tokens ---------------
