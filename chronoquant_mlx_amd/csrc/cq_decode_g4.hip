@@ -41,8 +41,8 @@ constexpr int kG4 = 4;  // q heads per kv head this kernel serves
 
 // Code rows of the chunk being computed, by token (row kChunk: junk), rows
 // padded to 20 words so that 16 consecutive rows start on distinct 4-bank
-// groups: the pipelined instance loads a chunk's P-frame rows as contiguous
-// blocks and scatters them here to their tokens.
+// groups: the pipelined and balanced instances load a chunk's P-frame rows
+// as contiguous blocks and scatter them here to their tokens.
 constexpr int kRowWords = 20;
 struct alignas(16) G4Rows {
   uint32_t k[kChunk + 1][kRowWords];
@@ -442,10 +442,11 @@ struct G4Buf {
 template <bool kBalanced, bool kOneChunk = false>
 __global__ __launch_bounds__(kThreadsMfma) void decode_g4_kernel(DecodeArgs a) {
   static_assert(!(kBalanced && kOneChunk), "one-chunk splits are a grid plan");
-  // Code loads: contiguous blocks scattered through LDS (the pipelined
-  // instance, where they are off the critical path), or each lane's own
-  // token rows (one-chunk splits and the balanced plan).
-  constexpr bool kContig = !kBalanced && !kOneChunk;
+  // Code loads: contiguous blocks scattered through LDS (the chunk loops of
+  // the pipelined and balanced instances, where they are off the critical
+  // path), or each lane's own token rows (one-chunk splits, whose single
+  // chunk would wait for the LDS round trip).
+  constexpr bool kContig = !kOneChunk;
   __shared__ G4Lds<kContig> lds;
   __shared__ int32_t s_units[kBalanced ? kMaxTableSeqs + 1 : 1];
   // Balanced plan: workgroup p of the column takes units [floor(pU/P),
@@ -556,7 +557,8 @@ __global__ __launch_bounds__(kThreadsMfma) void decode_g4_kernel(DecodeArgs a) {
     // Scatter targets (LDS words) of this lane's pieces of the contiguous code
     // blocks: piece j holds slot row s = 16j + lane / 4 (relative to base),
     // quarter lane % 4.  A computed chunk starts at c0 = 0 mod 64 (splits
-    // start at multiples of the split length, itself a multiple of 64), so
+    // start at multiples of the split length, itself a multiple of 64, and
+    // balanced segments at multiples of the 512-token unit), so
     // the P-frame token of row s depends on s alone: for strides below 64
     // (c0 an I-frame) t = s + (s - 1) / (stride - 1), s >= 1; for larger
     // strides t = s.  Rows of other tokens go to the junk row.  Rows of
