@@ -159,6 +159,31 @@ def test_pipelined_plan_strides(sk, sv):
         assert_tight(out[b], O.sdpa_fused(q[b], ck, cv, scale), what=f"b={b}")
 
 
+@pytest.mark.parametrize("sk,sv", [(4, 8), (8, 4), (16, 32), (64, 32), (128, 16), (64, 64)])
+def test_balanced_plan_strides(sk, sv):
+    # Ragged lengths over 8 kv heads take the balanced partition, whose
+    # instance also loads a chunk's code rows as contiguous slot blocks and
+    # scatters them to their tokens: strides below, at and above the chunk,
+    # segments that start inside a sequence at a 512-token unit boundary,
+    # and sequences that end inside a chunk.
+    rng = np.random.default_rng(sk * 1000 + sv + 7)
+    B, H, T, D, G = 12, 8, 3000, 128, 4
+    k = np.cumsum(rng.standard_normal((B, H, T, D)) * 0.1, axis=2).astype(np.float16)
+    v = np.cumsum(rng.standard_normal((B, H, T, D)) * 0.1, axis=2).astype(np.float16)
+    q = rng.standard_normal((B, G * H, D)).astype(np.float16)
+    lens = rng.integers(1, T + 1, size=B)
+    lens[:4] = [T, 1, 513, 2049]
+    params = dict(stride_k=sk, stride_v=sv)
+    cache = build_gpu_cache(k, v, **params)
+    scale = D ** -0.5
+    out = decode_gpu(cache, q, scale, seq_lens=lens.tolist())
+    for b, L in enumerate(lens.tolist()):
+        ck, cv = build_oracle(k[b, :, :L], v[b, :, :L], **params)
+        assert_tight(out[b], O.sdpa_fused(q[b], ck, cv, scale), what=f"b={b} L={L}")
+        if b < 3:
+            assert_close(out[b], oracle_fallback(ck, cv, q[b], scale), what=f"b={b} L={L}")
+
+
 def test_pipelined_plan_single_split():
     # 40 sequences x 8 kv heads fill the grid without splitting: one
     # workgroup per (sequence, kv head) over 640 tokens, so the pipelined
