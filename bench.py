@@ -93,11 +93,24 @@ def clone_cache(cache):
     return c
 
 
+def whole_cycles(steps, n):
+    """Launches timed for `steps` requested over n replicas: whole cycles of
+    the replicas (at least one), so that every replica counted in the
+    distinct bytes is read the same number of times."""
+    return max(1, -(-steps // n)) * n
+
+
+# launches the last time_graph / time_eager call timed (whole replica cycles)
+LAST_LAUNCHES = {"n": 0}
+
+
 def time_graph(launch_fns, steps, warmup, stream):
-    """Capture `steps` launches (cycling launch_fns) in a graph; replay once
-    for warmup, then time one replay with events on `stream`."""
+    """Capture whole cycles of launch_fns (at least `steps` launches) in a
+    graph; replay once for warmup, then time one replay with events on
+    `stream`.  Returns ms per launch over the launches captured."""
     import torch
     n = len(launch_fns)
+    launches = whole_cycles(steps, n)
     # warm up on the capture stream: the library sizes that stream's split
     # workspace outside capture
     stream.wait_stream(torch.cuda.current_stream())
@@ -107,7 +120,7 @@ def time_graph(launch_fns, steps, warmup, stream):
     torch.cuda.synchronize()
     g = torch.cuda.CUDAGraph()
     with torch.cuda.graph(g, stream=stream):
-        for i in range(steps):
+        for i in range(launches):
             launch_fns[i % n]()
     g.replay()
     torch.cuda.synchronize()
@@ -118,14 +131,17 @@ def time_graph(launch_fns, steps, warmup, stream):
         g.replay()
         e1.record(stream)
     e1.synchronize()
-    return e0.elapsed_time(e1) / steps  # ms per launch
+    LAST_LAUNCHES["n"] = launches
+    return e0.elapsed_time(e1) / launches  # ms per launch
 
 
 def time_eager(launch_fns, steps, warmup, stream):
-    """Launch `steps` times (cycling launch_fns) without a graph, bracketed by
-    events on `stream` (for profilers that count per dispatch)."""
+    """Launch whole cycles of launch_fns (at least `steps` launches) without a
+    graph, bracketed by events on `stream` (for profilers that count per
+    dispatch).  Returns ms per launch."""
     import torch
     n = len(launch_fns)
+    launches = whole_cycles(steps, n)
     with torch.cuda.stream(stream):
         for i in range(max(warmup, 1)):
             launch_fns[i % n]()
@@ -133,11 +149,21 @@ def time_eager(launch_fns, steps, warmup, stream):
         e0 = torch.cuda.Event(enable_timing=True)
         e1 = torch.cuda.Event(enable_timing=True)
         e0.record(stream)
-        for i in range(steps):
+        for i in range(launches):
             launch_fns[i % n]()
         e1.record(stream)
     e1.synchronize()
-    return e0.elapsed_time(e1) / steps
+    LAST_LAUNCHES["n"] = launches
+    return e0.elapsed_time(e1) / launches
+
+
+def cycle_record(algo_bytes, replicas):
+    """What the timed launches read: the replicas' distinct bytes and their
+    ratio to the 256 MB Infinity Cache, and the launches timed."""
+    distinct = int(algo_bytes) * int(replicas)
+    return {"replicas": int(replicas), "launches_timed": LAST_LAUNCHES["n"],
+            "distinct_bytes_cycled": distinct,
+            "distinct_bytes_over_infinity_cache": round(distinct / MALL_BYTES, 2)}
 
 
 def copy_calibration(dev, nbytes=256 << 20, reps=4):
@@ -292,7 +318,8 @@ def time_decode_config(name, dev, stream, steps, warmup, timer, device_gen):
                        f"dz {cfg.dead_zone_k}/{cfg.dead_zone_v}",
            "us_per_layer": round(ms * 1e3, 3), "GBps": round(gbs, 1),
            "frac": round(gbs / HBM_PEAK_GBS, 4), "algorithmic_bytes_per_step": algo,
-           "replicas": reps, "data": "on-GPU AR(1) generator" if device_gen else "seeded AR(1)"}
+           **cycle_record(algo, reps),
+           "data": "on-GPU AR(1) generator" if device_gen else "seeded AR(1)"}
     del caches, cache
     torch.cuda.empty_cache()
     return res
@@ -608,7 +635,7 @@ def main():
     import torch
 
     from chronoquant_mlx_amd import _lib, synth
-    from chronoquant_mlx_amd.kernels import chronoquant_sdpa_kernel
+    from chronoquant_mlx_amd.kernels import chronoquant_sdpa_cache_kernel
 
     cfg = synth.CONFIGS[args.config]
     dev = torch.device("cuda:0")
@@ -648,7 +675,7 @@ def main():
     ms = timer([mk(d) for d in descs], args.steps, args.warmup, stream)
     gbs = algo_bytes / (ms * 1e-3) / 1e9
     # correctness of the timed kernel against the eager call
-    ref = chronoquant_sdpa_kernel(q, cache, scale)
+    ref = chronoquant_sdpa_cache_kernel(q, cache, scale)
     torch.cuda.synchronize()
     log(f"[bench] decode {ms * 1e3:.2f} us/layer, {gbs:.0f} GB/s")
 
@@ -670,7 +697,7 @@ def main():
                                f"D={cfg.head_dim} T={cfg.T} strides {cfg.stride_k}/{cfg.stride_v} "
                                f"INT{cfg.delta_bits_k}/INT{cfg.delta_bits_v} (seeded AR(1) fp16 K/V)",
                    "algorithmic_bytes_per_step": algo_bytes,
-                   "replicas": reps},
+                   **cycle_record(algo_bytes, reps)},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
                      "traffic": measured_traffic(cfg.name)},

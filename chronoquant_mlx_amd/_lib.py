@@ -16,6 +16,7 @@ LIB_PATH = os.path.join(PKG, "libchronoquant.so")
 HEADER = os.path.join(os.path.dirname(PKG), "include", "chronoquant.h")
 
 CQ_OK = 0
+CQ_ERR_TIMEOUT = 10
 CQ_F16, CQ_BF16, CQ_F32 = 0, 1, 2
 CQ_KEYS, CQ_VALUES = 0, 1
 
@@ -87,6 +88,8 @@ SIGNATURES = {
     "cq_qkv_rope_append": ([_DESC, _P, _P, _P, _P, _P, _P, _I64, _P, _I64, _I32, _F, _I32, _P,
                             _I64, _P, _P], _I32),
     "cq_silu_mul": ([_P, _P, _I64, _I64, _I32, _P], _I32),
+    "cq_decode_status": ([_P, _P], _I32),
+    "cq_set_fold_poll_bound": ([_I32], _I32),
     "cq_status_string": ([_I32], ctypes.c_char_p),
 }
 
@@ -144,6 +147,26 @@ def require_gpu(t: torch.Tensor) -> None:
 
 def stream_of(t: torch.Tensor) -> int:
     return torch.cuda.current_stream(t.device).cuda_stream
+
+
+_hip = None
+
+
+def stream_capture_id(stream_handle: int) -> int | None:
+    """Id of the stream capture in progress on a hipStream_t, None when the
+    stream is not capturing.  Asks the HIP runtime the process already has
+    loaded (torch's), through hipStreamGetCaptureInfo."""
+    global _hip
+    if _hip is None:
+        _hip = ctypes.CDLL("libamdhip64.so", mode=os.RTLD_NOLOAD)
+        _hip.hipStreamGetCaptureInfo.argtypes = [_P, ctypes.POINTER(ctypes.c_int),
+                                                 ctypes.POINTER(ctypes.c_ulonglong)]
+        _hip.hipStreamGetCaptureInfo.restype = ctypes.c_int
+    status, cid = ctypes.c_int(0), ctypes.c_ulonglong(0)
+    err = _hip.hipStreamGetCaptureInfo(stream_handle, ctypes.byref(status), ctypes.byref(cid))
+    if err != 0:
+        raise RuntimeError(f"hipStreamGetCaptureInfo failed with error {err}")
+    return int(cid.value) if status.value == 1 else None  # hipStreamCaptureStatusActive
 
 
 def ptr(t) -> int | None:

@@ -18,7 +18,7 @@ from __future__ import annotations
 
 import torch
 
-from .kernels import (MAX_FUSED_HEAD_DIM, chronoquant_prefill_kernel, chronoquant_sdpa_kernel,
+from .kernels import (MAX_FUSED_HEAD_DIM, chronoquant_prefill_kernel, chronoquant_sdpa_cache_kernel,
                       prefill_supported)
 
 # q_len > 1 with mask None / "causal" runs the gfx950 chunked-prefill kernel
@@ -43,7 +43,9 @@ def _apply_mask(scores: torch.Tensor, mask):
 
 
 def chronoquant_sdpa(queries: torch.Tensor, keys, values, cache, scale: float, mask=None):
-    """ChronoQuant SDPA with fused generation path and reconstruct fallback.
+    """Attention over a ChronoQuantCache: the fused decode kernel for one
+    query token, the chunked-prefill kernel, or GPU reconstruction + dense
+    attention for everything else.
 
     queries: [B, n_q_heads, q_len, D]; keys/values are the placeholders
     update_and_fetch returned (attention reads the cache).
@@ -64,7 +66,7 @@ def chronoquant_sdpa(queries: torch.Tensor, keys, values, cache, scale: float, m
                          "(one query token, mask None, use_fused)")
     if use_fused:
         q = queries.reshape(batch, n_q_heads, head_dim)
-        out = chronoquant_sdpa_kernel(q, cache, scale, seq_lens=cache._dev_len)
+        out = chronoquant_sdpa_cache_kernel(q, cache, scale, seq_lens=cache._dev_len)
         return out.reshape(batch, n_q_heads, q_len, head_dim)
 
     if PREFILL_KERNEL and prefill_supported(queries, cache, mask):

@@ -54,6 +54,9 @@ _WORKSPACES: dict = {}
 # Workspaces replaced by larger ones.  A captured HIP graph keeps the address
 # it was captured with, so a replaced workspace is never freed.
 _RETIRED: list = []
+# Workspaces allocated under stream capture, one per capture (key: device,
+# stream, capture id); kept for the life of the process with their graphs.
+_CAPTURE_WORKSPACES: dict = {}
 
 
 def _shared_workspace(device: torch.device, nbytes: int) -> torch.Tensor:
@@ -62,25 +65,33 @@ def _shared_workspace(device: torch.device, nbytes: int) -> torch.Tensor:
 
     The kernels return its counters to zero, so it is reused without
     clearing.  Calls on one stream are ordered, so they never overlap on
-    it; calls on another stream use another workspace.  Under stream
-    capture a missing (or too small) workspace is allocated from the
-    graph's memory pool; its zero fill is a kernel captured with it, so every
-    replay starts from zeroed counters.
+    it; calls on another stream use another workspace.
+
+    Under stream capture a graph gets a workspace of its own, allocated from
+    the graph's memory pool at its first use in the capture (the zero fill is
+    a kernel captured with it, so every replay starts from zeroed counters)
+    and shared only by the calls of that capture.  A capture never reuses the
+    stream's eager workspace (a graph may be replayed on another stream,
+    concurrently with eager calls) and eager calls never see a capture's.
     """
     stream = torch.cuda.current_stream(device)
-    key = (device.index, stream.cuda_stream)
-    ws = _WORKSPACES.get(key)
+    handle = stream.cuda_stream
+    cid = _lib.stream_capture_id(handle) if torch.cuda.is_current_stream_capturing() else None
+    table = _WORKSPACES if cid is None else _CAPTURE_WORKSPACES
+    key = (device.index, handle) if cid is None else (device.index, handle, cid)
+    ws = table.get(key)
     if ws is None or ws.numel() < nbytes:
         old = 0 if ws is None else ws.numel()
         new = torch.zeros(max(nbytes, 1 << 20, 2 * old), dtype=torch.uint8, device=device)
         if ws is not None:
             _RETIRED.append(ws)
-        _WORKSPACES[key] = ws = new
+        table[key] = ws = new
     return ws
 
 
 class ChronoQuantCache:
-    """ChronoQuant KV cache with packed INT4 deltas and fused attention path."""
+    """KV cache of fp16 anchors (every stride-th token) and INT4-coded
+    residual rows for the tokens between them, read by the fused decode."""
 
     def __init__(
         self,
@@ -394,7 +405,8 @@ class ChronoQuantCache:
         return out
 
     def reconstruct_history(self):
-        """Reconstruct full K/V history for fallback attention paths."""
+        """fp16 K and V of every cached token, [B, H, offset, D] each, for the
+        attention paths that do not read the compressed rows directly."""
         return self._reconstruct_component("k"), self._reconstruct_component("v")
 
     # ------------------------------------------------------------------

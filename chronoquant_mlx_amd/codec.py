@@ -49,15 +49,16 @@ class ChronoQuantCodec:
         _lib.call("cq_quantize_delta", delta.data_ptr(), _lib.dtype_code(delta.dtype), rows, D,
                   self.delta_bits, float(self.dead_zone_ratio), codes.data_ptr(),
                   scales.data_ptr(), _lib.stream_of(delta))
+        # every _log_interval-th call: the share of zero codes in this call
+        # (a host sync, as the reference's counter does)
         self._call_count += 1
         if self._log_interval and self._call_count % self._log_interval == 0:
-            n_total = codes.numel()
-            n_zero = int((codes == 0).sum().item())
-            self._total_elements += n_total
-            self._zero_elements += n_zero
-            sparsity = n_zero / max(n_total, 1)
-            print(f"  [codec] bits={self.delta_bits} dz={self.dead_zone_ratio:.2f} "
-                  f"sparsity={sparsity:.1%} ({n_zero}/{n_total} zeros)")
+            zeros = int((codes == 0).sum().item())
+            self._total_elements += codes.numel()
+            self._zero_elements += zeros
+            print(f"  [codec] {self.delta_bits}-bit residuals, dead zone "
+                  f"{self.dead_zone_ratio:.2f}: {zeros / max(codes.numel(), 1):.1%} of "
+                  f"{codes.numel()} codes are zero")
         return codes, scales
 
     def dequantize_delta(self, codes: torch.Tensor, scale: torch.Tensor) -> torch.Tensor:

@@ -652,6 +652,9 @@ const char *cq_status_string(int32_t status) {
     case CQ_ERR_SCRATCH:
       return "shape needs more split workspace than the static scratch holds "
              "(CQ_NOALLOC_SCRATCH_BYTES); use cq_decode_attn with a workspace";
+    case CQ_ERR_TIMEOUT:
+      return "a split wait of an earlier decode ran out of poll rounds and folded without "
+             "every partial (its output is unreliable); the workspace has been cleared";
     default: return "unknown status";
   }
 }

@@ -216,13 +216,20 @@ static int lpt_log2_for(int W) {
   return l;
 }
 
+static std::atomic<int> g_poll_rounds{kDefaultPollRounds};
+
+int current_poll_rounds() { return g_poll_rounds.load(std::memory_order_relaxed); }
+
 int64_t split_tokens_override() {
   static const int64_t v = [] {
     const char *e = getenv("CQ_DECODE_SPLIT_TOKENS");
     if (!e || !*e) return (int64_t)0;
     char *end = nullptr;
     const long long x = strtoll(e, &end, 10);
-    return (end && *end == 0 && x > 0 && x % 64 == 0 && x <= (1 << 24)) ? (int64_t)x : (int64_t)0;
+    // whole split granules only: every kernel's split plan assumes them
+    return (end && *end == 0 && x > 0 && x % kSplitGranule == 0 && x <= (1 << 24))
+               ? (int64_t)x
+               : (int64_t)0;
   }();
   return v;
 }
@@ -410,6 +417,36 @@ int cq_decode_attn_noalloc(const cq_cache_desc *cache, const void *q, int32_t q_
   if (st) return st;
   return decode_entry(cache, q, q_dtype, n_q_heads, scale, seq_lens, seq_len, max_seq_len, out,
                       out_dtype, ws, kScratchBytes, stream, true);
+}
+
+int cq_decode_status(void *workspace, cq_stream_t stream) {
+  if (!workspace) {
+    const int st = current_scratch(&workspace);
+    if (st) return st;
+  }
+  if ((uintptr_t)workspace & 255) return CQ_ERR_ALIGN;
+  const hipStream_t s = (hipStream_t)stream;
+  uint32_t word = 0;
+  if (hipStreamSynchronize(s) != hipSuccess ||
+      hipMemcpy(&word, (char *)workspace + kStatusOffset, sizeof(word), hipMemcpyDeviceToHost) !=
+          hipSuccess) {
+    (void)hipGetLastError();
+    return CQ_ERR_LAUNCH;
+  }
+  if (word == 0) return CQ_OK;
+  // every kernel of the stream has finished, so no late split store can land
+  // after this clear
+  if (hipMemsetAsync(workspace, 0, kCounterRegion, s) != hipSuccess ||
+      hipStreamSynchronize(s) != hipSuccess) {
+    (void)hipGetLastError();
+    return CQ_ERR_LAUNCH;
+  }
+  return CQ_ERR_TIMEOUT;
+}
+
+int32_t cq_set_fold_poll_bound(int32_t rounds) {
+  return g_poll_rounds.exchange(rounds < 1 ? kDefaultPollRounds : rounds,
+                                std::memory_order_relaxed);
 }
 
 int cq_fp16_decode_attn(const uint16_t *k, const uint16_t *v, int64_t cap_tokens,

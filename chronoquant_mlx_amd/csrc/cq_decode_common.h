@@ -46,7 +46,9 @@ struct DecodeArgs {
   uint32_t *recs;      // [B][H][nsplit][64 units] fold records (GQA-4 grid plan); null: unused
   int nsplit;
   int64_t split_len;
-  int lpt_log2;  // portable kernel: lanes per token = 1 << lpt_log2 (>= W)
+  int lpt_log2;     // portable kernel: lanes per token = 1 << lpt_log2 (>= W)
+  int poll_rounds;  // bound of the split waits (fold records, split-ready flags)
+  uint32_t *status; // sticky status word of the workspace (kStatus* bits)
 };
 
 // Kernel arguments are read through the scalar cache, which every dispatch
@@ -379,8 +381,8 @@ int64_t mfma_max_resident();     // max over the MFMA-file kernels
 int64_t decode_max_resident();   // max over every decode kernel
 
 // Tokens per split forced by the environment variable CQ_DECODE_SPLIT_TOKENS
-// (a positive multiple of 64, read once per process; 0 when unset or
-// invalid).  A tuning knob for split-count sweeps: every grid plan then uses
+// (a positive multiple of kSplitGranule, read once per process; 0 when unset
+// or invalid).  A tuning knob for split-count sweeps: every grid plan then uses
 // splits of that length, and uniform batches keep the grid plan.
 int64_t split_tokens_override();
 
@@ -427,7 +429,17 @@ constexpr int64_t kMaxRecSplits = 512;  // (sequence, kv head, split) triples
 constexpr size_t kRecBytes = (size_t)kMaxRecSplits * kRecUnits * kRecWords * sizeof(uint32_t);
 constexpr size_t kCounterRegion = kCounterBytes + kFlagBytes + kRecBytes;
 constexpr int64_t kMaxCounters = kCounterBytes / sizeof(uint32_t);
-constexpr int64_t kMaxFlags = kFlagBytes / sizeof(uint32_t);
+// The last 256 bytes of the flag area hold the workspace's sticky status
+// word: a split wait that ran out of poll rounds sets kStatusFoldTimeout
+// there (its fold went ahead without the missing partials, and a late split
+// may then have left its record or flag set in the zero region).
+// cq_decode_status reads it and, when set, clears the whole zero region.
+constexpr size_t kStatusOffset = kCounterBytes + kFlagBytes - 256;
+constexpr int64_t kMaxFlags = (kFlagBytes - 256) / sizeof(uint32_t);
+constexpr uint32_t kStatusFoldTimeout = 1u;
+// Poll rounds of a split wait unless a test lowers them (cq_set_fold_poll_bound).
+constexpr int kDefaultPollRounds = 1 << 20;
+int current_poll_rounds();
 
 inline size_t round256(size_t x) { return (x + 255) / 256 * 256; }
 
@@ -439,6 +451,8 @@ inline size_t workspace_bytes_for(int B, int nq, int D, int nsplit) {
 
 inline void carve_workspace(DecodeArgs &a, void *ws) {
   char *p = (char *)ws;
+  a.status = (uint32_t *)(p + kStatusOffset);
+  a.poll_rounds = current_poll_rounds();
   a.counters = (uint32_t *)p;
   a.flags = (int64_t)a.B * a.H * a.nsplit <= kMaxFlags ? (uint32_t *)(p + kCounterBytes) : nullptr;
   a.recs = nullptr;  // the GQA-4 grid launcher opts in (records_of)
@@ -472,7 +486,8 @@ inline int setup_workspace(DecodeArgs &a, void *workspace, size_t ws_bytes) {
     carve_workspace(a, workspace);
   } else {
     a.part_ml = a.part_acc = nullptr;
-    a.counters = a.flags = a.recs = nullptr;
+    a.counters = a.flags = a.recs = a.status = nullptr;
+    a.poll_rounds = 0;
   }
   return CQ_OK;
 }

@@ -219,7 +219,14 @@ __device__ __forceinline__ float group_sum(float v, int lg) {
   return v;
 }
 
-constexpr int kRecPollRounds = 1 << 20;
+// A split wait that ran out of poll rounds: set the workspace's sticky
+// status (the fold goes ahead with what it has; cq_decode_status reports the
+// event to the host and clears the zero region).  Lane 0 of the waiting wave.
+__device__ __forceinline__ void note_poll_timeout(const DecodeArgs &a) {
+  if ((threadIdx.x & 63) == 0)
+    __hip_atomic_fetch_or(a.status, kStatusFoldTimeout, __ATOMIC_RELAXED,
+                          __HIP_MEMORY_SCOPE_AGENT);
+}
 
 // Wave 0 of split f's workgroup folds its units; lane = (unit k of the pass,
 // split s), 2^lg >= live lanes per unit.
@@ -239,7 +246,8 @@ __device__ __forceinline__ void fold_records_g4(const DecodeArgs &a, int b, int 
     const uint32_t off =
         (uint32_t)(((col * a.nsplit + s) * kRecUnits + (valid ? u : 0)) * (kRecWords * 4));
     uint4 hv = uint4{0u, 0u, 0u, 0u}, o0 = hv, o1 = hv;
-    for (int round = 0; round < kRecPollRounds; ++round) {
+    int round = 0;
+    for (; round < a.poll_rounds; ++round) {
       if (valid) {
         hv = load_rec4(rr, off);
         o0 = load_rec4(rr, off + 16u);
@@ -250,6 +258,7 @@ __device__ __forceinline__ void fold_records_g4(const DecodeArgs &a, int b, int 
       if (__all(ok)) break;
       __builtin_amdgcn_s_sleep(1);
     }
+    if (round == a.poll_rounds) note_poll_timeout(a);
     const float m = valid ? rec_value(hv.x) : -INFINITY;
     const float M = group_max(m, lg);
     const float w = (m == -INFINITY) ? 0.f : fast_exp2(m - M);
@@ -288,12 +297,14 @@ __device__ __forceinline__ void fold_records_g4(const DecodeArgs &a, int b, int 
 // sleeping between rounds; the other waves wait at the barrier.  The other
 // splits of the sequence are running workgroups of the same grid (the plans
 // launch one resident generation) that publish their partials without
-// waiting on anything, so the wait ends; kPollRounds bounds it regardless.
-constexpr int kPollRounds = 1 << 20;
-__device__ __forceinline__ void wait_split_flags(const uint32_t *fl, int live) {
+// waiting on anything, so the wait ends; a.poll_rounds bounds it regardless
+// (and a wait that runs out sets the workspace's sticky status).
+__device__ __forceinline__ void wait_split_flags(const DecodeArgs &a, const uint32_t *fl,
+                                                 int live) {
   if (threadIdx.x < 64) {
     const int lane = threadIdx.x;
-    for (int round = 0; round < kPollRounds; ++round) {
+    int round = 0;
+    for (; round < a.poll_rounds; ++round) {
       bool ready = true;
       for (int sp = 1 + lane; sp < live; sp += 64)
         ready = ready && __hip_atomic_load(const_cast<uint32_t *>(fl) + sp, __ATOMIC_RELAXED,
@@ -301,6 +312,7 @@ __device__ __forceinline__ void wait_split_flags(const uint32_t *fl, int live) {
       if (__all(ready)) break;
       __builtin_amdgcn_s_sleep(1);
     }
+    if (round == a.poll_rounds) note_poll_timeout(a);
   }
   __syncthreads();
 }
@@ -389,7 +401,7 @@ __device__ __forceinline__ void merge_finish_g4(const DecodeArgs &a, G4Merge &M,
       if (tid == 0) __hip_atomic_store(fl + slot, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       return;
     }
-    wait_split_flags(fl, live);
+    wait_split_flags(a, fl, live);
     merge_partials_g4(a, racc, rml, bq0, gn, live);
     for (int sp = 1 + tid; sp < live; sp += kThreadsMfma)
       __hip_atomic_store(fl + sp, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -628,6 +640,9 @@ __global__ __launch_bounds__(kThreadsMfma) void decode_g4_kernel(DecodeArgs a) {
         for (int kb = 0; kb < 4; ++kb) cb.ka[kb] = bload128(r_kfk, row + 16u * kb);
       }
       if constexpr (!kContig) {
+        // the slots other lanes stored above (no instruction at wave scope;
+        // it orders the LDS store before the loads)
+        wave_lds_sync();
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const int4 sl4 = *(const int4 *)&W.slot_v[16 * i + 4 * kg];

@@ -112,13 +112,13 @@ __device__ __forceinline__ uint32_t dpp_u(uint32_t v) {
                                                 0xf, false);
 }
 
-// max(a, b) of non-NaN values as one v_max_f32: fmaxf in IEEE mode first
+// max(a, b) of non-NaN values as one instruction: fmaxf in IEEE mode first
 // canonicalises every operand the compiler cannot prove canonical (values
-// moved across lanes, converted halves), one extra VALU each.
+// moved across lanes, converted halves), one extra VALU each; the IEEE
+// 754-2019 maximum (NaN-propagating) needs no canonical operands and is one
+// v_maximum3_f32 on gfx950.
 __device__ __forceinline__ float max_nn(float a, float b) {
-  float r;
-  asm("v_max_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
-  return r;
+  return __builtin_elementwise_maximum(a, b);
 }
 __device__ __forceinline__ float wave_max(float v) {
   v = fmaxf(v, dpp_f<kDppQuadXor1>(v));

@@ -91,11 +91,10 @@ __device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
 
 __device__ __forceinline__ h2_t as_h2(uint32_t u) { return __builtin_bit_cast(h2_t, u); }
 // Packed fp16 max of non-NaN pairs, without the canonicalising moves the
-// compiler puts around v_pk_max_f16 in IEEE mode.
+// compiler puts around v_pk_max_f16 in IEEE mode: the IEEE 754-2019 maximum,
+// one v_pk_maximum3_f16 on gfx950.
 __device__ __forceinline__ h2_t pk_max_nn(h2_t a, h2_t b) {
-  h2_t r;
-  asm("v_pk_max_f16 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
-  return r;
+  return __builtin_elementwise_maximum(a, b);
 }
 __device__ __forceinline__ uint32_t as_u(h2_t h) { return __builtin_bit_cast(uint32_t, h); }
 __device__ __forceinline__ h8_t h8_of(uint32_t a, uint32_t b, uint32_t c, uint32_t d) {

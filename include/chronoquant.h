@@ -8,7 +8,10 @@
  *     memory; scratch space is an explicit workspace argument);
  *   - is stream ordered and asynchronous (work is enqueued on `stream`, a
  *     hipStream_t passed as void*; NULL means the legacy default stream);
- *   - is re-entrant for distinct buffers and streams (no global mutable state).
+ *   - is re-entrant for distinct buffers and streams.  The library's global
+ *     state is limited to per-device caches filled once (occupancy figures,
+ *     the address of cq_decode_attn_noalloc's static scratch), that scratch
+ *     itself, and the test hook cq_set_fold_poll_bound.
  *
  * Storage layout (identical to the reference's logical tensors; an outer
  * capacity dimension per (sequence, kv head) lets appends write in place):
@@ -43,7 +46,8 @@ enum cq_status {
   CQ_ERR_WORKSPACE = 6,   /* workspace missing or smaller than required */
   CQ_ERR_UNSUPPORTED = 7, /* valid request the library does not implement */
   CQ_ERR_LAUNCH = 8,      /* kernel launch reported an error */
-  CQ_ERR_SCRATCH = 9      /* shape needs more than the static scratch holds */
+  CQ_ERR_SCRATCH = 9,     /* shape needs more than the static scratch holds */
+  CQ_ERR_TIMEOUT = 10     /* an earlier decode's split wait ran out (cq_decode_status) */
 };
 
 enum cq_dtype { CQ_F16 = 0, CQ_BF16 = 1, CQ_F32 = 2 };
@@ -167,6 +171,30 @@ int cq_decode_attn_noalloc(const cq_cache_desc *cache, const void *q, int32_t q_
                            int32_t n_q_heads, float scale, const int32_t *seq_lens,
                            int64_t seq_len, int64_t max_seq_len, void *out,
                            int32_t out_dtype, cq_stream_t stream);
+
+/* Split waits.  The decode kernels of one-generation grids (every workgroup
+ * of the launch resident at once, which the split plans size for) let each
+ * split wait, with a bounded poll, for the partials of the other splits of
+ * its sequence.  Co-residency is what HIP launches of one resident
+ * generation give on an idle device; it is not guaranteed when other kernels
+ * occupy the CUs (for instance two decodes running at once on different
+ * streams).  A wait that runs out of poll rounds folds what it has and sets
+ * a sticky status word in the workspace.
+ *
+ * cq_decode_status synchronises `stream` and reads that word: CQ_OK when no
+ * wait ran out since the last query, else CQ_ERR_TIMEOUT, after clearing the
+ * workspace's split state (counters, flags, fold records and the word) so
+ * that later calls are correct again.  The outputs of the calls since the
+ * previous query are then unreliable.  workspace: a cq_decode_attn
+ * workspace, or NULL for the current device's cq_decode_attn_noalloc
+ * scratch.  Not callable under stream capture (it synchronises).  No
+ * counterpart in the reference (whose Metal kernel has no split waits). */
+int cq_decode_status(void *workspace, cq_stream_t stream);
+
+/* Test hook: the poll rounds of every later split wait (rounds < 1 restores
+ * the default, 2^20).  Returns the previous bound.  Process-wide; for tests
+ * that force a wait to run out while every kernel still exits normally. */
+int32_t cq_set_fold_poll_bound(int32_t rounds);
 
 /* Same contract as cq_decode_attn but always runs the portable (VALU) decode
  * kernel, for any head_dim <= 256 and q dtype; the test suite uses it to

@@ -23,7 +23,7 @@ def test_library_exports_every_header_symbol():
 
 def test_status_strings():
     assert _lib.status_string(0) == "ok"
-    for s in range(1, 9):
+    for s in range(1, 11):
         assert _lib.status_string(s) != "unknown status"
     assert _lib.status_string(99) == "unknown status"
 

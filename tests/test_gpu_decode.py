@@ -20,10 +20,10 @@ pytestmark = pytest.mark.gpu
 
 
 def decode_gpu(cache, q_np, scale, generic=False, seq_lens=None):
-    from chronoquant_mlx_amd.kernels import chronoquant_sdpa_kernel
+    from chronoquant_mlx_amd.kernels import chronoquant_sdpa_cache_kernel
     q = to_gpu(q_np)
     lens = None if seq_lens is None else torch.tensor(seq_lens, dtype=torch.int32, device="cuda")
-    return chronoquant_sdpa_kernel(q, cache, scale, seq_lens=lens, generic=generic).float().cpu().numpy()
+    return chronoquant_sdpa_cache_kernel(q, cache, scale, seq_lens=lens, generic=generic).float().cpu().numpy()
 
 
 def oracle_fallback(ck, cv, q_b, scale):
@@ -307,7 +307,7 @@ def test_uniform_batch_ranges_across_sequences(G):
 
 
 def test_output_dtypes_and_fp32_queries():
-    from chronoquant_mlx_amd.kernels import chronoquant_sdpa_kernel
+    from chronoquant_mlx_amd.kernels import chronoquant_sdpa_cache_kernel
     rng = np.random.default_rng(5)
     B, H, T, D = 1, 2, 300, 128
     k = np.cumsum(rng.standard_normal((B, H, T, D)) * 0.1, axis=2).astype(np.float16)
@@ -322,13 +322,13 @@ def test_output_dtypes_and_fp32_queries():
     # fp32 output: no output rounding; what remains is the fp16 rounding of the
     # softmax weights fed to the MFMA P.V (<= 2^-12 relative per weight, the
     # rounding point the reference fallback also has) and fp32 accumulation
-    out32 = chronoquant_sdpa_kernel(to_gpu(q), cache, 0.3, out_dtype=torch.float32)
+    out32 = chronoquant_sdpa_cache_kernel(to_gpu(q), cache, 0.3, out_dtype=torch.float32)
     assert_close(out32[0].cpu().numpy(), fused, 5e-5, 2.5e-4)
-    out32g = chronoquant_sdpa_kernel(to_gpu(q), cache, 0.3, out_dtype=torch.float32, generic=True)
+    out32g = chronoquant_sdpa_cache_kernel(to_gpu(q), cache, 0.3, out_dtype=torch.float32, generic=True)
     assert_close(out32g[0].cpu().numpy(), fused, 2e-5, 1e-5)  # portable kernel: fp32 weights
     # fp32 queries: q*scale is not rounded to fp16; compare with binary64
     # attention on the reconstruction
-    outq = chronoquant_sdpa_kernel(to_gpu(q, torch.float32), cache, 0.3).cpu().numpy()
+    outq = chronoquant_sdpa_cache_kernel(to_gpu(q, torch.float32), cache, 0.3).cpu().numpy()
     exact = O.sdpa_exact(q[0], ck.reconstruct(), cv.reconstruct(), 0.3)
     assert_close(outq[0], exact)
 
@@ -340,7 +340,7 @@ def test_split_fold_outputs_and_short_bound_lengths(out_dtype):
     # device length shorter than the cache, so that fewer splits than the
     # plan's hold tokens: T=3000 gives 6 splits of 512 tokens, length 1300
     # leaves 3 of them live.
-    from chronoquant_mlx_amd.kernels import chronoquant_sdpa_kernel
+    from chronoquant_mlx_amd.kernels import chronoquant_sdpa_cache_kernel
     dt = {"f16": torch.float16, "bf16": torch.bfloat16, "f32": torch.float32}[out_dtype]
     rng = np.random.default_rng(31 + len(out_dtype))
     B, H, T, D, G = 1, 8, 3000, 128, 4
@@ -354,7 +354,7 @@ def test_split_fold_outputs_and_short_bound_lengths(out_dtype):
     atol, rtol = {"f16": (5e-4, 2e-3), "bf16": (2e-3, 8e-3), "f32": (5e-5, 2.5e-4)}[out_dtype]
     for L in (T, 1300):
         lens = None if L == T else torch.tensor([L], dtype=torch.int32, device="cuda")
-        out = chronoquant_sdpa_kernel(to_gpu(q), cache, scale, out_dtype=dt,
+        out = chronoquant_sdpa_cache_kernel(to_gpu(q), cache, scale, out_dtype=dt,
                                       seq_lens=lens).float().cpu().numpy()
         ck, cv = build_oracle(k[0][:, :L], v[0][:, :L], **params)
         assert_close(out[0], oracle_fallback(ck, cv, q[0], scale), what=f"{out_dtype} L={L}")
@@ -431,7 +431,7 @@ def test_bf16_queries():
     # the MFMA kernel as fp16 (exact in fp16's normal range) and to the
     # portable kernel as fp32; both against binary64 attention on the fp16
     # reconstruction with the same q'
-    from chronoquant_mlx_amd.kernels import chronoquant_sdpa_kernel
+    from chronoquant_mlx_amd.kernels import chronoquant_sdpa_cache_kernel
     rng = np.random.default_rng(17)
     B, H, T, D, G = 2, 2, 900, 128, 4
     k = np.cumsum(rng.standard_normal((B, H, T, D)) * 0.1, axis=2).astype(np.float16)
@@ -441,8 +441,8 @@ def test_bf16_queries():
     cache = build_gpu_cache(k, v, **params)
     scale = D ** -0.5
     qb = torch.from_numpy(q32).to("cuda").to(torch.bfloat16)
-    out_m = chronoquant_sdpa_kernel(qb, cache, scale).float().cpu().numpy()
-    out_g = chronoquant_sdpa_kernel(qb, cache, scale, generic=True).float().cpu().numpy()
+    out_m = chronoquant_sdpa_cache_kernel(qb, cache, scale).float().cpu().numpy()
+    out_g = chronoquant_sdpa_cache_kernel(qb, cache, scale, generic=True).float().cpu().numpy()
     scb = torch.tensor(scale, dtype=torch.bfloat16)
     qprime = (qb.cpu() * scb).to(torch.float16).numpy()  # bf16 product, exactly representable
     for b in range(B):

@@ -62,11 +62,11 @@ def test_append_streaming(g, name):
 
 @pytest.mark.parametrize("name", ATTN)
 def test_decode(g, name):
-    from chronoquant_mlx_amd.kernels import chronoquant_sdpa_kernel
+    from chronoquant_mlx_amd.kernels import chronoquant_sdpa_cache_kernel
     (H, nq, T, D), p = params(g, name)
     cache = build_gpu_cache(g[f"{name}/k"][None], g[f"{name}/v"][None], **p)
     q = to_gpu(g[f"{name}/q"][None])
-    out = chronoquant_sdpa_kernel(q, cache, D ** -0.5).float().cpu().numpy()[0]
+    out = chronoquant_sdpa_cache_kernel(q, cache, D ** -0.5).float().cpu().numpy()[0]
     assert_close(out, g[f"{name}/out_fallback"].astype(np.float64), what=name)
     mfma = D == 128 and min(p["stride_k"], p["stride_v"]) >= 4  # the MFMA kernel's domain
     assert_tight(out, g[f"{name}/out_fused"], what=name, mfma=mfma)

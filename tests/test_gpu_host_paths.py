@@ -123,7 +123,7 @@ def test_torch_graph_recipe(prefill):
     # torch.cuda.graph(g) (torch's own capture stream, whose split workspace
     # is then allocated under capture); replays with other library calls
     # between them must each equal the eager result
-    from chronoquant_mlx_amd.kernels import chronoquant_prefill_kernel, chronoquant_sdpa_kernel
+    from chronoquant_mlx_amd.kernels import chronoquant_prefill_kernel, chronoquant_sdpa_cache_kernel
     H, G, T, D = 8, 4, 3000, 128
     k, v = _data(40 + prefill, H, T, D)
     cache = build_gpu_cache(k, v, stride_k=32, stride_v=8)
@@ -133,7 +133,7 @@ def test_torch_graph_recipe(prefill):
         run = lambda: chronoquant_prefill_kernel(q, cache, D ** -0.5, causal=True)
     else:
         q = to_gpu(rng.standard_normal((1, G * H, D)))
-        run = lambda: chronoquant_sdpa_kernel(q, cache, D ** -0.5)
+        run = lambda: chronoquant_sdpa_cache_kernel(q, cache, D ** -0.5)
     ref = run().clone()
     side = torch.cuda.Stream()
     side.wait_stream(torch.cuda.current_stream())
@@ -151,4 +151,4 @@ def test_torch_graph_recipe(prefill):
         g.replay()
         torch.cuda.synchronize()
         assert torch.equal(out.view(torch.int16), ref.view(torch.int16))
-        chronoquant_sdpa_kernel(q2, other, D ** -0.5)  # eager work between the replays
+        chronoquant_sdpa_cache_kernel(q2, other, D ** -0.5)  # eager work between the replays

@@ -31,7 +31,7 @@ def _same_state(a, b):
                                     dict(stride_k=1, stride_v=8)])
 def test_round_trip_then_continue(tmp_path, params):
     from chronoquant_mlx_amd import load_prompt_cache, save_prompt_cache
-    from chronoquant_mlx_amd.kernels import chronoquant_sdpa_kernel
+    from chronoquant_mlx_amd.kernels import chronoquant_sdpa_cache_kernel
     B, H, T, D = 2, 4, 400, 128
     k, v = _kv(3, B, H, T + 100, D)
     a = build_gpu_cache(k[:, :, :T], v[:, :, :T], **params)
@@ -43,8 +43,8 @@ def test_round_trip_then_continue(tmp_path, params):
         (a.stride_k, a.stride_v, a.delta_bits_v, a.dead_zone_v)
     _same_state(a, b)
     q = to_gpu(np.random.default_rng(4).standard_normal((B, 4 * H, D)).astype(np.float16))
-    oa = chronoquant_sdpa_kernel(q, a, D ** -0.5)
-    ob = chronoquant_sdpa_kernel(q, b, D ** -0.5)
+    oa = chronoquant_sdpa_cache_kernel(q, a, D ** -0.5)
+    ob = chronoquant_sdpa_cache_kernel(q, b, D ** -0.5)
     assert torch.equal(oa, ob)
     # appending to the reloaded cache continues exactly where the saved one was
     kn, vn = to_gpu(k[:, :, T:]), to_gpu(v[:, :, T:])
@@ -91,7 +91,7 @@ def test_dense_file_reloads_the_same_cache(tmp_path, params):
     import os
 
     from chronoquant_mlx_amd import load_prompt_cache, save_prompt_cache
-    from chronoquant_mlx_amd.kernels import chronoquant_sdpa_kernel
+    from chronoquant_mlx_amd.kernels import chronoquant_sdpa_cache_kernel
     B, H, T, D = 2, 4, 400, 128
     k, v = _kv(8, B, H, T, D)
     a = build_gpu_cache(k, v, **params)
@@ -105,4 +105,4 @@ def test_dense_file_reloads_the_same_cache(tmp_path, params):
     saved = sum(n_pf[c] * (64 - D * bits[c] // 8) for c in "kv" if bits[c] < 4)
     assert os.path.getsize(f_int4) - os.path.getsize(f_dense) - saved in range(-256, 256)
     q = to_gpu(np.random.default_rng(9).standard_normal((B, 4 * H, D)).astype(np.float16))
-    assert torch.equal(chronoquant_sdpa_kernel(q, a, D ** -0.5), chronoquant_sdpa_kernel(q, b, D ** -0.5))
+    assert torch.equal(chronoquant_sdpa_cache_kernel(q, a, D ** -0.5), chronoquant_sdpa_cache_kernel(q, b, D ** -0.5))
