@@ -68,9 +68,10 @@ def build_cache(cfg, dev):
     return cache, k, v, kt, vt
 
 
-def build_cache_device(cfg, dev, capacity=None):
+def build_cache_device(cfg, dev, capacity=None, dense=False):
     """Cache filled from the on-GPU generator (workloads too large for the
-    host generator); same AR(1) statistics, different random streams."""
+    host generator); same AR(1) statistics, different random streams.
+    dense: 2- and 3-bit residual rows stored at their width (dense_residuals)."""
     import torch
 
     from chronoquant_mlx_amd import ChronoQuantCache, synth
@@ -78,7 +79,7 @@ def build_cache_device(cfg, dev, capacity=None):
     cache = ChronoQuantCache(stride_k=cfg.stride_k, stride_v=cfg.stride_v,
                              delta_bits_k=cfg.delta_bits_k, delta_bits_v=cfg.delta_bits_v,
                              dead_zone_k=cfg.dead_zone_k, dead_zone_v=cfg.dead_zone_v,
-                             capacity=capacity or cfg.T)
+                             capacity=capacity or cfg.T, dense_residuals=dense)
     cache.update_and_fetch(kt, vt)
     torch.cuda.synchronize()
     return cache, kt, vt
@@ -280,21 +281,26 @@ def time_torch_sdpa(cfg, kvs, q, scale, stream, steps, warmup, timer, check_agai
             "fastest": best, "runs": runs}
 
 
-def time_decode_config(name, dev, stream, steps, warmup, timer, device_gen):
+def time_decode_config(name, dev, stream, steps, warmup, timer, device_gen, dense=False):
     """Fused decode of one configuration (full context, every sequence at T):
-    us/layer and algorithmic GB/s over cycled cache replicas."""
+    us/layer and algorithmic GB/s over cycled cache replicas.  dense: the
+    cache's 2- and 3-bit residual rows at their width (algorithmic bytes are
+    then that cache's nbytes + Q + O)."""
     import torch
 
     from chronoquant_mlx_amd import _lib, synth
     cfg = synth.CONFIGS[name]
     if device_gen:
-        cache, kt, vt = build_cache_device(cfg, dev)
+        cache, kt, vt = build_cache_device(cfg, dev, dense=dense)
     else:
+        assert not dense
         cache, _, _, kt, vt = build_cache(cfg, dev)
     del kt, vt
     q = torch.randn(cfg.B, cfg.n_q_heads, cfg.head_dim, device=dev).half()
     scale = cfg.head_dim ** -0.5
     algo = synth.algorithmic_decode_bytes(cfg)
+    if dense:
+        algo = cache.nbytes + 2 * q.numel() * 2
     reps = replica_count(cache.nbytes)
     caches = [cache] + [clone_cache(cache) for _ in range(reps - 1)]
     out = torch.empty(cfg.B, cfg.n_q_heads, cfg.head_dim, dtype=torch.float16, device=dev)
@@ -320,6 +326,8 @@ def time_decode_config(name, dev, stream, steps, warmup, timer, device_gen):
            "frac": round(gbs / HBM_PEAK_GBS, 4), "algorithmic_bytes_per_step": algo,
            **cycle_record(algo, reps),
            "data": "on-GPU AR(1) generator" if device_gen else "seeded AR(1)"}
+    if dense:
+        res["workload"] += "; dense 3-bit V rows (48 B) in HBM"
     del caches, cache
     torch.cuda.empty_cache()
     return res
@@ -753,6 +761,8 @@ def main():
                 / extra["ftv3_16k"]["us_per_layer"], 3)
         extra["c2"] = time_decode_config("c2", dev, stream, args.steps, args.warmup, timer,
                                          device_gen=True)
+        extra["c2_dense"] = time_decode_config("c2", dev, stream, args.steps, args.warmup, timer,
+                                               device_gen=True, dense=True)
         extra["c3"] = time_streaming("c3", dev, stream)
         extra["prefill"] = time_prefill(dev, stream, 50)
         if not args.no_e2e:

@@ -19,6 +19,7 @@ CQ_OK = 0
 CQ_ERR_TIMEOUT = 10
 CQ_F16, CQ_BF16, CQ_F32 = 0, 1, 2
 CQ_KEYS, CQ_VALUES = 0, 1
+CQ_PACK_INT4, CQ_PACK_DENSE = 0, 1
 
 _DTYPES = {torch.float16: CQ_F16, torch.bfloat16: CQ_BF16, torch.float32: CQ_F32}
 
@@ -41,7 +42,7 @@ class CqComponent(ctypes.Structure):
         ("stride", ctypes.c_int32),
         ("delta_bits", ctypes.c_int32),
         ("dead_zone", ctypes.c_float),
-        ("reserved", ctypes.c_int32),
+        ("packing", ctypes.c_int32),
     ]
 
 

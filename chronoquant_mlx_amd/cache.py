@@ -89,6 +89,26 @@ def _shared_workspace(device: torch.device, nbytes: int) -> torch.Tensor:
     return ws
 
 
+def dense_rows_of_int4(words: torch.Tensor, head_dim: int, bits: int) -> torch.Tensor:
+    """INT4-lane rows [..., ceil(D/8)] -> dense rows [..., ceil(D * bits / 32)]
+    (the layout CQ_PACK_DENSE components hold in HBM: the little-endian
+    stream of persist.dense_pack, zero-padded to whole words)."""
+    from .persist import dense_pack
+    stream = dense_pack(words.contiguous(), head_dim, bits)
+    rw = (head_dim * bits + 31) // 32
+    pad = 4 * rw - stream.shape[-1]
+    if pad:
+        stream = torch.nn.functional.pad(stream, (0, pad))
+    return stream.contiguous().view(torch.uint32)
+
+
+def int4_of_dense_rows(rows: torch.Tensor, head_dim: int, bits: int) -> torch.Tensor:
+    """Inverse of dense_rows_of_int4."""
+    from .persist import dense_unpack
+    nbytes = (head_dim * bits + 7) // 8
+    return dense_unpack(rows.contiguous().view(torch.uint8)[..., :nbytes], head_dim, bits)
+
+
 class ChronoQuantCache:
     """KV cache of fp16 anchors (every stride-th token) and INT4-coded
     residual rows for the tokens between them, read by the fused decode."""
@@ -105,6 +125,7 @@ class ChronoQuantCache:
         per_layer_v_bits: list = None,
         layer_idx: int = 0,
         capacity: int = 0,
+        dense_residuals: bool = False,
     ):
         if stride_k < 1 or stride_v < 1:
             raise ValueError("strides must be >= 1")
@@ -115,6 +136,9 @@ class ChronoQuantCache:
         self.dead_zone_k = dead_zone_k
         self.dead_zone_v = dead_zone_v
         self.use_fused = use_fused
+        # opt-in: 2- and 3-bit components keep their codes at their own width
+        # in HBM (this library's format; the reference's rows are INT4 lanes)
+        self.dense_residuals = bool(dense_residuals)
         self.per_layer_v_bits = per_layer_v_bits or []
         self.layer_idx = layer_idx
         self.codec_k = ChronoQuantCodec(stride=stride_k, delta_bits=delta_bits_k,
@@ -147,6 +171,22 @@ class ChronoQuantCache:
 
     def _stride(self, component: str) -> int:
         return self.stride_k if component == "k" else self.stride_v
+
+    def _bits(self, component: str) -> int:
+        return self.delta_bits_k if component == "k" else self._get_codec_for_v().delta_bits
+
+    def _packing(self, component: str) -> int:
+        """CQ_PACK_DENSE for a 2- or 3-bit component of a dense_residuals
+        cache, else CQ_PACK_INT4 (the reference's layout)."""
+        dense = self.dense_residuals and self._bits(component) < 4
+        return _lib.CQ_PACK_DENSE if dense else _lib.CQ_PACK_INT4
+
+    def _row_words(self, component: str) -> int:
+        """uint32 words of one packed row: ceil(D/8) in INT4 lanes, ceil(D *
+        bits / 32) for dense rows."""
+        D = self._shape[2]
+        fb = self._bits(component) if self._packing(component) == _lib.CQ_PACK_DENSE else 4
+        return (D * fb + 31) // 32
 
     # ------------------------------------------------------------------
     # active views (cache.py:63-85)
@@ -182,9 +222,9 @@ class ChronoQuantCache:
     # ------------------------------------------------------------------
     def _allocate(self, cap: int):
         B, H, D = self._shape
-        W = (D + 7) // 8
         dev = self._device
         for c in ("k", "v"):
+            W = self._row_words(c)
             s = self._stride(c)
             nkf = max(1, _num_keyframes(cap, s))
             npf = max(1, _num_pframes(cap, s))
@@ -242,6 +282,7 @@ class ChronoQuantCache:
             comp.stride = self._stride(c)
             comp.delta_bits = codecs[c].delta_bits
             comp.dead_zone = float(codecs[c].dead_zone_ratio)
+            comp.packing = self._packing(c)
         return ctypes.byref(d)
 
     def _decode_workspace(self, n_q_heads: int) -> torch.Tensor:
@@ -419,6 +460,8 @@ class ChronoQuantCache:
         return self._active_keyframes("v").squeeze(0)
 
     def _kernel_packed(self, c):
+        """(Dense rows for a dense_residuals component: the reference
+        operator's INT4 reading does not apply to them.)"""
         p = self._active_packed(c)
         if p is not None and p.shape[2] > 0:
             return p.squeeze(0)
@@ -455,6 +498,7 @@ class ChronoQuantCache:
         The reference (cache.py:220-234) omits a component's packed/scales pair
         while it has no P-frames, which makes a 4-tensor list ambiguous
         (stride_k=1); this cache always emits all six (empty when unused).
+        A dense_residuals component's packed tensor holds its dense rows.
         """
         if self.offset == 0 or self._kf["k"] is None:
             return []
@@ -465,7 +509,10 @@ class ChronoQuantCache:
     @state.setter
     def state(self, values):
         """Restore from a state list (cache.py:236-255).  Six tensors are read
-        in the order above; shorter lists follow the reference's reading."""
+        in the order above; shorter lists follow the reference's reading.
+        Packed rows may be INT4 words (the reference's state) or, for a
+        dense_residuals component, its dense rows; INT4 words given to a dense
+        component are converted."""
         if not values:
             return
         kf_k, kf_v = values[0], values[1]
@@ -497,14 +544,17 @@ class ChronoQuantCache:
         self._sc = {"k": None, "v": None}
         self._cap = 0
         self._ensure_capacity(max(offset, 1))
-        W = (D + 7) // 8
         for c, kf, pk, sc in (("k", kf_k, pk_k, sc_k), ("v", kf_v, pk_v, sc_v)):
             self._kf[c][:, :, : kf.shape[2]].copy_(kf.to(torch.float16))
             n_pf = _num_pframes(offset, self._stride(c))
             if n_pf:
-                if pk is None or pk.shape[2] != n_pf or pk.shape[3] != W:
+                rw = self._row_words(c)
+                if pk is None or pk.shape[2] != n_pf or pk.shape[3] not in (rw, (D + 7) // 8):
                     raise ValueError(f"state is missing the {c} P-frames")
-                self._pk[c][:, :, :n_pf].copy_(pk.view(torch.uint32) if pk.dtype == torch.int32 else pk)
+                pk = pk.view(torch.uint32) if pk.dtype == torch.int32 else pk
+                if pk.shape[3] != rw:  # INT4 words for a dense component
+                    pk = dense_rows_of_int4(pk.to(self._device), D, self._bits(c))
+                self._pk[c][:, :, :n_pf].copy_(pk)
                 self._sc[c][:, :, :n_pf].copy_(sc.reshape(B, H, n_pf).to(torch.float16))
         self.offset = offset
         self._max_len = offset

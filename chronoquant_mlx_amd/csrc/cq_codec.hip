@@ -220,6 +220,30 @@ __device__ __forceinline__ void load_cache_anchor(const cq_component &c, int64_t
   }
 }
 
+// Word `lane` of a dense row (fb-bit fields, fb < 4) held by a wave whose
+// lane l has the codes of dims l*E .. l*E + E - 1: lane l's fields form the
+// E*fb stream bits from E*fb*l, and word w ORs the (at most 32/(E*fb) + 2)
+// lanes whose bits meet [32w, 32w + 32).  Dims past D give 0 bits.  Called
+// by the whole wave (the shuffles read every lane).
+__device__ __forceinline__ uint32_t dense_row_word(const int (&code)[kMaxE], int E, int fb,
+                                                   int lane, int D) {
+  const int cb = E * fb;  // stream bits per lane
+  uint32_t chunk = 0;
+#pragma unroll
+  for (int i = 0; i < kMaxE; ++i)
+    if (i < E && lane * E + i < D) chunk |= code_field(code[i], fb) << (fb * i);
+  const int j0 = (32 * lane) / cb;
+  const int n = 32 / cb + 2;  // wave-uniform
+  uint32_t word = 0;
+  for (int k = 0; k < n; ++k) {
+    const int j = j0 + k;
+    const uint32_t cj = (uint32_t)__shfl((int)chunk, j & 63, 64);
+    const int sh = cb * j - 32 * lane;
+    if (j < 64 && sh < 32 && sh > -cb) word |= sh >= 0 ? cj << sh : cj >> (-sh);
+  }
+  return word;
+}
+
 // Encode one token row whose operands are loaded: the fp16 I-frame when t is
 // a multiple of the stride (reference cache.py:103-105), else the residual
 // against anchor g (cache.py:107-116: d = round(token - round(anchor))),
@@ -250,10 +274,17 @@ __device__ __forceinline__ void encode_token(const cq_component &c, const TokenR
   for (int i = 0; i < kMaxE; ++i) d[i] = Dt<DT>::round(r.v[i] - Dt<DT>::round(r.an[i]));
   int code[kMaxE];
   const float sc = codec_row<DT>(d, E, c.delta_bits, c.dead_zone, code);
-  const uint32_t word = pack_lane(code, E, lane, D);
-  const int wl = lane * E;
-  if ((wl & 7) == 0 && (wl >> 3) < W)
-    c.packed[(bh * c.cap_pframes + slot) * W + (wl >> 3)] = word;
+  const int fb = field_bits(c);
+  if (fb == 4) {
+    const uint32_t word = pack_lane(code, E, lane, D);
+    const int wl = lane * E;
+    if ((wl & 7) == 0 && (wl >> 3) < W)
+      c.packed[(bh * c.cap_pframes + slot) * W + (wl >> 3)] = word;
+  } else {
+    const int rw = row_words_of(D, fb);
+    const uint32_t word = dense_row_word(code, E, fb, lane, D);
+    if (lane < rw) c.packed[(bh * c.cap_pframes + slot) * rw + lane] = word;
+  }
   if (lane == 0) c.scales[bh * c.cap_pframes + slot] = f2h(sc);
 }
 
@@ -429,6 +460,8 @@ __global__ __launch_bounds__(256) void append_row4_kernel(AppendArgs a) {
     const int64_t cap_pf = ci ? a.comp[1].cap_pframes : a.comp[0].cap_pframes;
     const int stride = ci ? a.comp[1].stride : a.comp[0].stride;
     const int bits = ci ? a.comp[1].delta_bits : a.comp[0].delta_bits;
+    const int fb = ci ? field_bits(a.comp[1]) : field_bits(a.comp[0]);
+    const int rw = row_words_of(128, fb);
     const float dz = ci ? a.comp[1].dead_zone : a.comp[0].dead_zone;
     const uint16_t *x = (const uint16_t *)(ci ? a.x[1] : a.x[0]);
     const int64_t xs0 = ci ? a.xs[1][0] : a.xs[0][0], xs1 = ci ? a.xs[1][1] : a.xs[0][1],
@@ -469,15 +502,21 @@ __global__ __launch_bounds__(256) void append_row4_kernel(AppendArgs a) {
       int code[8];
       const float scale = codec_row16<DT>(d, bits, dz, code);
       const int64_t slot = t - g - 1;
-      if (ok && slot < cap_pf) {
-        uint32_t word = 0;
+      // this lane's 8 fields (8 fb stream bits from 8 fb j); a dense row's
+      // word j takes them from lanes j1 = 32j / 8fb and j1 + 1 of the row
+      // (the row's 16 lanes share this branch)
+      uint32_t chunk = 0;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          int u = code[i] + 8;
-          u = u < 0 ? 0 : (u > 15 ? 15 : u);
-          word |= (uint32_t)u << (4 * i);
-        }
-        pk[(bh * cap_pf + slot) * 16 + j] = word;
+      for (int i = 0; i < 8; ++i) chunk |= code_field(code[i], fb) << (fb * i);
+      uint32_t word = chunk;
+      if (fb != 4) {
+        const int j1 = (32 * j) / (8 * fb), o = (32 * j) % (8 * fb);
+        const uint32_t lo = (uint32_t)__shfl((int)chunk, (lane & 48) + min(j1, 15), 64);
+        const uint32_t hi = (uint32_t)__shfl((int)chunk, (lane & 48) + min(j1 + 1, 15), 64);
+        word = (lo >> o) | (hi << (8 * fb - o));
+      }
+      if (ok && slot < cap_pf) {
+        if (j < rw) pk[(bh * cap_pf + slot) * rw + j] = word;
         if (j == 0) sc[bh * cap_pf + slot] = f2h(scale);
       }
     }
@@ -588,19 +627,24 @@ __global__ __launch_bounds__(256) void reconstruct_kernel(cq_component c, int B,
   const bool is_p = (t - g * c.stride) != 0;
   const uint16_t *anc = c.keyframes + (bh * c.cap_keyframes + g) * D;
   uint16_t *o = out + bht * D;
-  uint32_t word = 0;
+  const int fb = field_bits(c), rw = row_words_of(D, fb);
+  uint32_t fields = 0;  // the 8 fields of dims 8w .. 8w + 7
   float s = 0.f;
   if (is_p) {
     const int64_t slot = t - g - 1;
-    word = c.packed[(bh * c.cap_pframes + slot) * W + w];
+    fields = stream_bits(c.packed + (bh * c.cap_pframes + slot) * rw, rw, 8 * fb * w, 8 * fb);
     s = h2f(c.scales[bh * c.cap_pframes + slot]);
   }
+  const uint32_t mask = (1u << fb) - 1u;
 #pragma unroll
   for (int k = 0; k < 8; ++k) {
     const int dim = 8 * w + k;
     if (dim >= D) break;
     float delta = 0.f;
-    if (is_p) delta = h2f(f2h((float)((int)((word >> (4 * k)) & 0xfu) - 8) * s));
+    if (is_p) {
+      const int code = (int)((fields >> (fb * k)) & mask) - (1 << (fb - 1));
+      delta = h2f(f2h((float)code * s));
+    }
     o[dim] = f2h(h2f(anc[dim]) + delta);  // fp16 add, cache.py:156
   }
 }
@@ -625,6 +669,7 @@ int validate_cache(const cq_cache_desc *c) {
     if (p->stride < 1 || !bits_ok(p->delta_bits)) return CQ_ERR_ARG;
     if (!(p->dead_zone >= 0.f)) return CQ_ERR_ARG;
     if (p->cap_keyframes < 1 || p->cap_pframes < 1) return CQ_ERR_CAPACITY;
+    if (p->packing != CQ_PACK_INT4 && p->packing != CQ_PACK_DENSE) return CQ_ERR_ARG;
   }
   return CQ_OK;
 }

@@ -58,10 +58,14 @@ __device__ __forceinline__ void dequant8(const DecodeArgs &a, int ci, int64_t bh
   load_row8(a.kf[ci] + (bh * a.cap_kf[ci] + g) * a.D, w, a.D, x);
   if (t - g * stride != 0) {
     const int64_t slot = t - g - 1;
-    const uint32_t word = a.pk[ci][(bh * a.cap_pf[ci] + slot) * a.W + w];
+    const int fb = a.fbits[ci], rw = row_words_of(a.D, fb);
+    // the fields of dims 8w .. 8w + 7 (one word of an INT4 row)
+    const uint32_t f8 = stream_bits(a.pk[ci] + (bh * a.cap_pf[ci] + slot) * rw, rw, 8 * fb * w, 8 * fb);
     const float s = h2f(a.sc[ci][bh * a.cap_pf[ci] + slot]);
+    const uint32_t mask = (1u << fb) - 1u;
+    const int bias = 1 << (fb - 1);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) x[i] += (float)((int)((word >> (4 * i)) & 0xfu) - 8) * s;
+    for (int i = 0; i < 8; ++i) x[i] += (float)((int)((f8 >> (fb * i)) & mask) - bias) * s;
   }
 }
 
@@ -266,7 +270,7 @@ int64_t decode_max_resident() { return std::max(generic_resident(), mfma_max_res
 static int launch_generic(DecodeArgs &a, void *workspace, size_t ws_bytes, hipStream_t stream) {
   int st = prepare_launch(a, kGenericGroup, generic_resident(), workspace, ws_bytes);
   if (st) return st;
-  a.lpt_log2 = lpt_log2_for(a.W);
+  a.lpt_log2 = (int16_t)lpt_log2_for(a.W);
   const dim3 grid((unsigned)a.nsplit, (unsigned)(a.H * a.n_chunks), (unsigned)a.B);
   decode_generic_kernel<<<grid, dim3(256), 0, stream>>>(a);
   return hipGetLastError() == hipSuccess ? CQ_OK : CQ_ERR_LAUNCH;
@@ -290,6 +294,7 @@ static int fill_decode_args(DecodeArgs &a, const cq_cache_desc *c, const void *q
     a.cap_pf[i] = cp[i]->cap_pframes;
     a.stride[i] = cp[i]->stride;
     a.inv_stride[i] = 1.0f / (float)cp[i]->stride;
+    a.fbits[i] = (int8_t)field_bits(*cp[i]);
     if (num_keyframes(max_T, cp[i]->stride) > cp[i]->cap_keyframes ||
         num_pframes(max_T, cp[i]->stride) > cp[i]->cap_pframes)
       return CQ_ERR_CAPACITY;
@@ -474,6 +479,7 @@ int cq_fp16_decode_attn(const uint16_t *k, const uint16_t *v, int64_t cap_tokens
     comp[i]->stride = 1;
     comp[i]->delta_bits = 4;
     comp[i]->dead_zone = 0.f;
+    comp[i]->packing = CQ_PACK_INT4;
   }
   return decode_entry(&c, q, q_dtype, n_q_heads, scale, seq_lens, seq_len, max_seq_len, out,
                       out_dtype, workspace, workspace_bytes, stream, true);

@@ -46,7 +46,8 @@ struct DecodeArgs {
   uint32_t *recs;      // [B][H][nsplit][64 units] fold records (GQA-4 grid plan); null: unused
   int nsplit;
   int64_t split_len;
-  int lpt_log2;     // portable kernel: lanes per token = 1 << lpt_log2 (>= W)
+  int16_t lpt_log2; // portable kernel: lanes per token = 1 << lpt_log2 (>= W)
+  int8_t fbits[2];  // stored field bits per component: 4 (INT4 lanes) or the dense width
   int poll_rounds;  // bound of the split waits (fold records, split-ready flags)
   uint32_t *status; // sticky status word of the workspace (kStatus* bits)
 };
@@ -512,7 +513,9 @@ inline int64_t balanced_slots(int64_t P, int64_t max_T) {
 
 int launch_decode_mfma(DecodeArgs &a, void *workspace, size_t ws_bytes, hipStream_t stream);
 bool mfma_supported(const DecodeArgs &a);
-// GQA groups of at most 4 q heads (cq_decode_g4.hip)
+// GQA groups of at most 4 q heads (cq_decode_g4.hip): the shape conditions
+// alone, and together with mfma_supported's
+bool g4_shape(const DecodeArgs &a);
 bool g4_supported(const DecodeArgs &a);
 int64_t g4_resident();
 int launch_decode_g4(DecodeArgs &a, void *workspace, size_t ws_bytes, hipStream_t stream);

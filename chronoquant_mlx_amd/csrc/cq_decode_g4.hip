@@ -451,9 +451,16 @@ struct G4Buf {
 // where it is as balanced as the partition below).  kBalanced = true: the
 // balanced partition of the batch's units (cq_plan.h), one or more segments
 // per workgroup.
-template <bool kBalanced, bool kOneChunk = false>
+//
+// kDenseV: the V rows are dense 3-bit rows (48 bytes: dim d's field code + 4
+// at stream bits 3d .. 3d + 2), see the V code products below.
+template <bool kBalanced, bool kOneChunk = false, bool kDenseV = false>
 __global__ __launch_bounds__(kThreadsMfma) void decode_g4_kernel(DecodeArgs a) {
   static_assert(!(kBalanced && kOneChunk), "one-chunk splits are a grid plan");
+  static_assert(!(kDenseV && kOneChunk), "dense V rows take the block-load instances");
+  // bytes of a V P-frame row, and its 1 KB blocks per 64-row chunk
+  constexpr uint32_t kVRow = kDenseV ? 48u : 64u;
+  constexpr int kVBlocks = kDenseV ? 3 : 4;
   // Code loads: contiguous blocks scattered through LDS (the chunk loops of
   // the pipelined and balanced instances, where they are off the critical
   // path), or each lane's own token rows (one-chunk splits, whose single
@@ -553,7 +560,7 @@ __global__ __launch_bounds__(kThreadsMfma) void decode_g4_kernel(DecodeArgs a) {
     const __amdgpu_buffer_rsrc_t r_pkk =
         make_rsrc(a.pk[0] + bh * a.cap_pf[0] * 16, (uint32_t)(a.cap_pf[0] * 64));
     const __amdgpu_buffer_rsrc_t r_pkv =
-        make_rsrc(a.pk[1] + bh * a.cap_pf[1] * 16, (uint32_t)(a.cap_pf[1] * 64));
+        make_rsrc(a.pk[1] + bh * a.cap_pf[1] * (kVRow / 4), (uint32_t)(a.cap_pf[1] * kVRow));
     const __amdgpu_buffer_rsrc_t r_sck = make_rsrc(a.sc[0] + bh * a.cap_pf[0], (uint32_t)(a.cap_pf[0] * 2));
     const __amdgpu_buffer_rsrc_t r_scv = make_rsrc(a.sc[1] + bh * a.cap_pf[1], (uint32_t)(a.cap_pf[1] * 2));
 
@@ -589,6 +596,17 @@ __global__ __launch_bounds__(kThreadsMfma) void decode_g4_kernel(DecodeArgs a) {
         wk[j] = scatter_word(j, lsk);
         wv[j] = scatter_word(j, lsv);
       }
+      if constexpr (kDenseV) {
+        // 48-byte rows: piece j of lane l is third (64j + l) % 3 of slot row
+        // (64j + l) / 3, written to words 4 * third of its token's row
+#pragma unroll
+        for (int j = 0; j < kVBlocks; ++j) {
+          const int pc = 64 * j + lane, sr = pc / 3;
+          int t = sr;
+          if (lsv < 6) t = sr == 0 ? kChunk : sr + (sr - 1) / ((1 << lsv) - 1);
+          wv[j] = min(t, kChunk) * kRowWords + 4 * (pc - 3 * sr);
+        }
+      }
     }
     auto stage = [&](int c0, G4Buf &cb) {
       const int nt = (int)max((int64_t)0, min((int64_t)kChunk, t1 - c0));
@@ -622,11 +640,11 @@ __global__ __launch_bounds__(kThreadsMfma) void decode_g4_kernel(DecodeArgs a) {
         // base + 63, base the slot token c0 would have (every P-frame row of
         // the chunk lies in them; rows before slot 0 or past the buffer read 0)
         const uint32_t bk = ((uint32_t)(c0 - gk_base - 1) * 64u + 16u * lane) | dead;
-        const uint32_t bv = ((uint32_t)(c0 - (c0 >> lsv) - 1) * 64u + 16u * lane) | dead;
+        const uint32_t bv = ((uint32_t)(c0 - (c0 >> lsv) - 1) * kVRow + 16u * lane) | dead;
 #pragma unroll
         for (int q = 0; q < 4; ++q) cb.kr[q] = bload128(r_pkk, bk + 1024u * q);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
+        for (int i = 0; i < kVBlocks; ++i) {
           const uint4 w = bload128(r_pkv, bv + 1024u * i);
           cb.vw[i][0] = w.x;
           cb.vw[i][1] = w.y;
@@ -718,6 +736,19 @@ __global__ __launch_bounds__(kThreadsMfma) void decode_g4_kernel(DecodeArgs a) {
 
     uint32_t magic;  // fp16 1024 in both halves, held in a VGPR for v_and_or_b32
     asm volatile("v_mov_b32 %0, 0x64006400" : "=v"(magic));
+    // dense V rows: the fp16 exponent fields of 2^(10 - pos), pos = 0 .. 7, in
+    // both halves (VGPRs, as magic)
+    uint32_t mg3[8];
+    if constexpr (kDenseV) {
+      asm volatile("v_mov_b32 %0, 0x64006400" : "=v"(mg3[0]));
+      asm volatile("v_mov_b32 %0, 0x60006000" : "=v"(mg3[1]));
+      asm volatile("v_mov_b32 %0, 0x5c005c00" : "=v"(mg3[2]));
+      asm volatile("v_mov_b32 %0, 0x58005800" : "=v"(mg3[3]));
+      asm volatile("v_mov_b32 %0, 0x54005400" : "=v"(mg3[4]));
+      asm volatile("v_mov_b32 %0, 0x50005000" : "=v"(mg3[5]));
+      asm volatile("v_mov_b32 %0, 0x4c004c00" : "=v"(mg3[6]));
+      asm volatile("v_mov_b32 %0, 0x48004800" : "=v"(mg3[7]));
+    }
 
     // score layout: softmax state of head hq (identical across its 16 lanes)
     float m_run = -INFINITY;  // log2 units
@@ -738,17 +769,30 @@ __global__ __launch_bounds__(kThreadsMfma) void decode_g4_kernel(DecodeArgs a) {
         // code rows by token: K row of this lane's token, V word col of tokens
         // 16i + 4kg + r
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          *(uint4 *)&W.rows.k[0][wk[j]] = cb.kr[j];
+        for (int j = 0; j < 4; ++j) *(uint4 *)&W.rows.k[0][wk[j]] = cb.kr[j];
+#pragma unroll
+        for (int j = 0; j < kVBlocks; ++j)
           *(uint4 *)&W.rows.v[0][wv[j]] = uint4{cb.vw[j][0], cb.vw[j][1], cb.vw[j][2], cb.vw[j][3]};
-        }
         wave_lds_sync();
 #pragma unroll
         for (int q = 0; q < 4; ++q) cb.kr[q] = *(const uint4 *)&W.rows.k[lane][4 * q];
+        if constexpr (kDenseV) {
+          // the 24 stream bits of dims 8col .. 8col + 7 (bytes 3col .. 3col + 2
+          // of the row) moved to bits 0 .. 23
+          const int w0 = (3 * col) >> 2, sh = 8 * ((3 * col) & 3);
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
+          for (int i = 0; i < 4; ++i)
 #pragma unroll
-          for (int r = 0; r < 4; ++r) cb.vw[i][r] = W.rows.v[16 * i + 4 * kg + r][col];
+            for (int r = 0; r < 4; ++r) {
+              const uint32_t *row = W.rows.v[16 * i + 4 * kg + r];
+              cb.vw[i][r] = __builtin_amdgcn_alignbit(row[w0 + 1], row[w0], sh);
+            }
+        } else {
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) cb.vw[i][r] = W.rows.v[16 * i + 4 * kg + r][col];
+        }
       }
       // ---- anchor table: log2e * q'.a - mref for anchors gk_base + 4kg + r ----------
       // (C[anchor][head col]; the lanes col < 4 are head col's score lanes of
@@ -842,18 +886,20 @@ __global__ __launch_bounds__(kThreadsMfma) void decode_g4_kernel(DecodeArgs a) {
         const h2_t sv01 = as_h2(__builtin_amdgcn_perm(s4.y, s4.x, 0x07060302u));
         const h2_t sv23 = as_h2(__builtin_amdgcn_perm(s4.w, s4.z, 0x07060302u));
         const h2_t w01 = p01 * sv01, w23 = p23 * sv23;
-        const h2_t x01 = w01 * sixteenth, x23 = w23 * sixteenth;
         l_run = __builtin_amdgcn_fdot2(p01, ones, l_run, false);
         l_run = __builtin_amdgcn_fdot2(p23, ones, l_run, false);
         w_run = __builtin_amdgcn_fdot2(w01, ones, w_run, false);
         w_run = __builtin_amdgcn_fdot2(w23, ones, w_run, false);
-        x_run = __builtin_amdgcn_fdot2(x01, ones, x_run, false);
-        x_run = __builtin_amdgcn_fdot2(x23, ones, x_run, false);
         // to the V-product operand layout: (head hq, 4-token group 4 jb + kg)
         const int g4 = 4 * jb + kg;
         W.pw[0][hq][g4] = uint2{__builtin_bit_cast(uint32_t, p01), __builtin_bit_cast(uint32_t, p23)};
         W.pw[1][hq][g4] = uint2{__builtin_bit_cast(uint32_t, w01), __builtin_bit_cast(uint32_t, w23)};
-        W.pw[2][hq][g4] = uint2{__builtin_bit_cast(uint32_t, x01), __builtin_bit_cast(uint32_t, x23)};
+        if constexpr (!kDenseV) {
+          const h2_t x01 = w01 * sixteenth, x23 = w23 * sixteenth;
+          x_run = __builtin_amdgcn_fdot2(x01, ones, x_run, false);
+          x_run = __builtin_amdgcn_fdot2(x23, ones, x_run, false);
+          W.pw[2][hq][g4] = uint2{__builtin_bit_cast(uint32_t, x01), __builtin_bit_cast(uint32_t, x23)};
+        }
       }
       wave_lds_sync();
 
@@ -867,18 +913,48 @@ __global__ __launch_bounds__(kThreadsMfma) void decode_g4_kernel(DecodeArgs a) {
       for (int P = 0; P < 2; ++P) {
         const uint2 pa = W.pw[0][hr][8 * P + kg], pb = W.pw[0][hr][8 * P + 4 + kg];
         const uint2 wa = W.pw[1][hr][8 * P + kg], wb = W.pw[1][hr][8 * P + 4 + kg];
-        const uint2 xa = W.pw[2][hr][8 * P + kg], xb = W.pw[2][hr][8 * P + 4 + kg];
         const h8_t ap = h8_of(pa.x, pa.y, pb.x, pb.y);
         const h8_t aw = h8_of(wa.x, wa.y, wb.x, wb.y);
-        const h8_t ax = h8_of(xa.x, xa.y, xb.x, xb.y);
         // E^T: group col x these tokens (fp16 1.0 = 0x3c00); each run of 4
         // tokens lies in one V group (stride >= 4)
         const int ga = ((c0 + 32 * P + 4 * kg) >> lsv) - gv_base;
         const int gb = ((c0 + 32 * P + 16 + 4 * kg) >> lsv) - gv_base;
         const uint32_t ea = ga == col ? 0x3c003c00u : 0u, eb = gb == col ? 0x3c003c00u : 0u;
         pg = mfma32(h8_of(ea, ea, eb, eb), ap, pg);
-        // V codes: B = 8 tokens x dim 8col + nb (nibble nb of word col)
         const int i0 = 2 * P, i1 = 2 * P + 1;
+        if constexpr (kDenseV) {
+          // V codes, dense rows: B = 8 tokens x dim 8col + e.  Byte pairs of
+          // a token pair's 24-bit groups (token r0 in the low half, r1 in the
+          // high half): bytes 0-1 hold fields 0, 1, 2 at bits 0, 3, 6; bytes
+          // 1-2 fields 3, 4, 5 at bits 1, 4, 7; byte 2 fields 6, 7 at bits 2,
+          // 5.  A field u at bit pos of a half, ORed with the fp16 exponent of
+          // 2^(10 - pos), is the fp16 value 2^(10 - pos) + u exactly.
+          uint32_t q0[4], q1[4], q2[4];
+#pragma unroll
+          for (int u = 0; u < 2; ++u)
+#pragma unroll
+            for (int m = 0; m < 2; ++m) {
+              const uint32_t xa = cb.vw[i0 + u][2 * m], xb = cb.vw[i0 + u][2 * m + 1];
+              q0[2 * u + m] = __builtin_amdgcn_perm(xb, xa, 0x05040100u);
+              q1[2 * u + m] = __builtin_amdgcn_perm(xb, xa, 0x06050201u);
+              q2[2 * u + m] = __builtin_amdgcn_perm(xb, xa, 0x0c060c02u);
+            }
+          auto vop = [&](const uint32_t(&q)[4], uint32_t m, uint32_t mg) {
+            return h8_of(and_or(q[0], m, mg), and_or(q[1], m, mg), and_or(q[2], m, mg),
+                         and_or(q[3], m, mg));
+          };
+          acc[0] = mfma32(aw, vop(q0, 0x00070007u, mg3[0]), acc[0]);
+          acc[1] = mfma32(aw, vop(q0, 0x00380038u, mg3[3]), acc[1]);
+          acc[2] = mfma32(aw, vop(q0, 0x01C001C0u, mg3[6]), acc[2]);
+          acc[3] = mfma32(aw, vop(q1, 0x000E000Eu, mg3[1]), acc[3]);
+          acc[4] = mfma32(aw, vop(q1, 0x00700070u, mg3[4]), acc[4]);
+          acc[5] = mfma32(aw, vop(q1, 0x03800380u, mg3[7]), acc[5]);
+          acc[6] = mfma32(aw, vop(q2, 0x001C001Cu, mg3[2]), acc[6]);
+          acc[7] = mfma32(aw, vop(q2, 0x00E000E0u, mg3[5]), acc[7]);
+        } else {
+        const uint2 xa = W.pw[2][hr][8 * P + kg], xb = W.pw[2][hr][8 * P + 4 + kg];
+        const h8_t ax = h8_of(xa.x, xa.y, xb.x, xb.y);
+        // V codes: B = 8 tokens x dim 8col + nb (nibble nb of word col)
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
           const uint32_t sel = (uint32_t)k | (0x0cu << 8) | ((uint32_t)(4 + k) << 16) | (0x0cu << 24);
@@ -892,6 +968,7 @@ __global__ __launch_bounds__(kThreadsMfma) void decode_g4_kernel(DecodeArgs a) {
                                  and_or(b01, 0x00F000F0u, magic), and_or(b23, 0x00F000F0u, magic));
           acc[2 * k] = mfma32(aw, blo, acc[2 * k]);
           acc[2 * k + 1] = mfma32(ax, bhi, acc[2 * k + 1]);
+        }
         }
       }
 
@@ -962,8 +1039,14 @@ __global__ __launch_bounds__(kThreadsMfma) void decode_g4_kernel(DecodeArgs a) {
     // head col's score lanes of block 0.  Code columns: x = 1032 + c (even nb,
     // weight p s) or 1152 + 16c (odd nb, weight p s / 16).
     merge_finish_g4(a, lds.mg, b, h, gn, slot, live, m_run, l_run, [&](int nb, int r) {
-      const float corr = (nb & 1) ? 1024.f * sx[r] + 8.f * sw[r] : 1032.f * sw[r];
-      return acc[nb][r] - corr;
+      if constexpr (kDenseV) {
+        // field u of dim 8col + nb entered as 2^(10 - pos) + u, code u - 4
+        constexpr float kOff[8] = {1028.f, 132.f, 20.f, 516.f, 68.f, 12.f, 260.f, 36.f};
+        return acc[nb][r] - kOff[nb] * sw[r];
+      } else {
+        const float corr = (nb & 1) ? 1024.f * sx[r] + 8.f * sw[r] : 1032.f * sw[r];
+        return acc[nb][r] - corr;
+      }
     });
     if constexpr (!kBalanced) return;
     __syncthreads();  // the next segment's merge reuses the merge area
@@ -973,10 +1056,12 @@ __global__ __launch_bounds__(kThreadsMfma) void decode_g4_kernel(DecodeArgs a) {
 // ---------------------------------------------------------------------------
 // host side
 // ---------------------------------------------------------------------------
-bool g4_supported(const DecodeArgs &a) {
+bool g4_shape(const DecodeArgs &a) {
   const bool pow2 = ((a.stride[0] & (a.stride[0] - 1)) | (a.stride[1] & (a.stride[1] - 1))) == 0;
-  return a.G <= kG4 && pow2 && a.stride[0] >= 4 && a.stride[1] >= 4 && mfma_supported(a);
+  return a.G <= kG4 && pow2 && a.stride[0] >= 4 && a.stride[1] >= 4;
 }
+
+bool g4_supported(const DecodeArgs &a) { return g4_shape(a) && mfma_supported(a); }
 
 int64_t g4_resident() {
   return resident_workgroups(reinterpret_cast<const void *>(decode_g4_kernel<true>), kThreadsMfma,
@@ -1021,12 +1106,16 @@ int launch_decode_g4(DecodeArgs &a, void *workspace, size_t ws_bytes, hipStream_
   const int64_t slots = (int64_t)a.B * a.H * a.nsplit;
   if (!balanced && a.nsplit > 1 && a.nsplit <= 64 && slots <= kMaxRecSplits && slots <= resident)
     a.recs = records_of(workspace);
+  const bool dense_v = a.fbits[1] == 3;  // (K rows are INT4: mfma_supported)
   if (balanced) {
     const dim3 grid((unsigned)P, (unsigned)a.H, 1u);
-    decode_g4_kernel<true><<<grid, dim3(kThreadsMfma), 0, stream>>>(a);
+    if (dense_v) decode_g4_kernel<true, false, true><<<grid, dim3(kThreadsMfma), 0, stream>>>(a);
+    else decode_g4_kernel<true><<<grid, dim3(kThreadsMfma), 0, stream>>>(a);
   } else {
     const dim3 grid((unsigned)a.nsplit, (unsigned)a.H, (unsigned)a.B);
-    if (a.split_len <= (int64_t)kWaves * kChunk)
+    if (dense_v)
+      decode_g4_kernel<false, false, true><<<grid, dim3(kThreadsMfma), 0, stream>>>(a);
+    else if (a.split_len <= (int64_t)kWaves * kChunk)
       decode_g4_kernel<false, true><<<grid, dim3(kThreadsMfma), 0, stream>>>(a);
     else
       decode_g4_kernel<false><<<grid, dim3(kThreadsMfma), 0, stream>>>(a);

@@ -603,6 +603,9 @@ static bool plain_mode(const DecodeArgs &a) { return a.stride[0] == 1 && a.strid
 
 bool mfma_supported(const DecodeArgs &a) {
   if (a.D != kD) return false;
+  // INT4 rows, or 3-bit dense V rows under the GQA-4 kernel's dense instance
+  if (a.fbits[0] != 4 || (a.fbits[1] != 4 && !(a.fbits[1] == 3 && g4_shape(a))))
+    return false;
   // compressed cache: fp16 or bf16 queries; fp16 baseline: fp16 queries
   if (a.q_dtype != CQ_F16 && !(a.q_dtype == CQ_BF16 && !plain_mode(a))) return false;
   if (a.max_T >= (1 << 24)) return false;

@@ -14,6 +14,33 @@ constexpr int kWave = 64;
 constexpr int kMaxHeadDim = 256;  // same limit as the reference's fused path
 
 // ---------------------------------------------------------------------------
+// Packed rows.  Dim d's code is stored as the fb-bit field code + 2^(fb-1)
+// at bits [fb*d, fb*d + fb) of the row's little-endian bit stream: fb = 4
+// for INT4 lanes (the reference's layout), delta_bits for dense rows.
+// ---------------------------------------------------------------------------
+__host__ __device__ inline int field_bits(const cq_component &c) {
+  return c.packing == CQ_PACK_DENSE ? c.delta_bits : 4;
+}
+__host__ __device__ inline int row_words_of(int D, int fb) { return (D * fb + 31) / 32; }
+__host__ __device__ inline int row_words(const cq_component &c, int D) {
+  return row_words_of(D, field_bits(c));
+}
+// n <= 32 stream bits starting at bit `bit` of a row of rw words (bits past
+// n, and past the row, read 0)
+__device__ __forceinline__ uint32_t stream_bits(const uint32_t *row, int rw, int bit, int n) {
+  const int w = bit >> 5, o = bit & 31;
+  uint32_t v = w < rw ? row[w] >> o : 0u;
+  if (o && o + n > 32 && w + 1 < rw) v |= row[w + 1] << (32 - o);
+  return n >= 32 ? v : v & ((1u << n) - 1u);
+}
+// an fb-bit field of a code: code + 2^(fb-1), clipped into the field
+__device__ __forceinline__ uint32_t code_field(int code, int fb) {
+  int u = code + (1 << (fb - 1));
+  const int top = (1 << fb) - 1;
+  return (uint32_t)(u < 0 ? 0 : (u > top ? top : u));
+}
+
+// ---------------------------------------------------------------------------
 // dtype traits.  round() rounds a binary32 value to the dtype (nearest even)
 // and returns it as binary32; every codec op is "compute in binary32, round"
 // which equals the dtype's own correctly rounded op for + - * / (24 >= 2p+2).

@@ -616,6 +616,8 @@ extern "C" int cq_prefill_attn(const cq_cache_desc *cache, const void *q, int32_
                                size_t workspace_bytes, cq_stream_t stream) {
   int st = validate_cache(cache);
   if (st) return st;
+  // dense residual rows: the reconstruct fallback serves them
+  if (field_bits(cache->k) != 4 || field_bits(cache->v) != 4) return CQ_ERR_UNSUPPORTED;
   if (!q || !out) return CQ_ERR_ARG;
   if (q_dtype != CQ_F16 && q_dtype != CQ_BF16) return CQ_ERR_DTYPE;
   if (cache->head_dim != kD) return CQ_ERR_UNSUPPORTED;

@@ -223,7 +223,8 @@ def chronoquant_prefill_kernel(q: torch.Tensor, cache, scale: float = 1.0,
 def prefill_supported(queries: torch.Tensor, cache, mask) -> bool:
     """Whether cq_prefill_attn serves this chronoquant_sdpa call."""
     B, nq, L, D = queries.shape
-    return (L > 1 and D == 128 and queries.dtype in (torch.float16, torch.bfloat16)
+    dense = any(cache._packing(c) != _lib.CQ_PACK_INT4 for c in ("k", "v"))
+    return (L > 1 and D == 128 and not dense and queries.dtype in (torch.float16, torch.bfloat16)
             and (mask is None or (isinstance(mask, str) and mask == "causal"))
             and cache.offset >= L and nq % cache._shape[1] == 0
             and 256 % (nq // cache._shape[1]) == 0)

@@ -79,12 +79,15 @@ def create_chronoquant_caches(
     dead_zone_v: float = 0.05,
     use_fused: bool = True,
     per_layer_v_bits: list = None,
+    dense_residuals: bool = False,
 ):
     """Replace every plain KVCache slot of the model's prompt cache with a
     ChronoQuantCache of these codec settings (patch.py:46-78).
 
     per_layer_v_bits: value residual width by layer index (layers past the
     end of the list take its last entry); None uses delta_bits_v everywhere.
+    dense_residuals (no reference counterpart, opt-in): 2- and 3-bit
+    components keep their codes at their own width in HBM.
     """
     caches = _base.make_prompt_cache(model)
     for index in range(len(caches)):
@@ -100,6 +103,7 @@ def create_chronoquant_caches(
                 dead_zone_v=dead_zone_v,
                 use_fused=use_fused,
                 per_layer_v_bits=per_layer_v_bits,
+                dense_residuals=dense_residuals,
             )
             caches[index].layer_idx = index  # selects its entry of per_layer_v_bits
     return caches
@@ -115,10 +119,11 @@ FULL_THROTTLE_V3_CONFIG = {  # patch.py:81-88
 }
 
 
-def create_full_throttle_caches(model, use_fused: bool = True):
+def create_full_throttle_caches(model, use_fused: bool = True, dense_residuals: bool = False):
     """Create the Full-Throttle V3 cache preset (patch.py:91-104).
 
-    3-bit V residuals still occupy INT4 lanes: the preset changes the code
-    range and the strides, not the byte layout.
+    3-bit V residuals occupy INT4 lanes, as in the reference, unless
+    dense_residuals (this library's opt-in) stores them as 48-byte rows.
     """
-    return create_chronoquant_caches(model, use_fused=use_fused, **FULL_THROTTLE_V3_CONFIG)
+    return create_chronoquant_caches(model, use_fused=use_fused, dense_residuals=dense_residuals,
+                                     **FULL_THROTTLE_V3_CONFIG)

@@ -16,9 +16,11 @@ file's metadata beside the layer's class name.
 Opt-in dense residuals (save_prompt_cache(..., dense=True)): a component
 whose residual codes have 2 or 3 bits stores them in the file as a bit stream
 of that width instead of the reference's INT4 lanes (3-bit: 48 instead of 64
-bytes per 128-dim row).  load_prompt_cache expands them back to INT4 lanes,
-so a loaded cache has the reference layout and every kernel path.  Such a
-file is this library's format only: the reference cannot read it.
+bytes per 128-dim row).  Such a file is this library's format only: the
+reference cannot read it.  The stream is the same one a dense_residuals
+cache holds in HBM (its rows are the stream padded to whole words), so such
+a cache saves its rows as they are; a cache loaded from the file takes the
+layout its own dense_residuals setting asks for.
 """
 from __future__ import annotations
 
@@ -98,7 +100,7 @@ def _dense_bits(c) -> dict:
 
 
 _PARAMS = ("stride_k", "stride_v", "delta_bits_k", "delta_bits_v", "dead_zone_k", "dead_zone_v",
-           "use_fused", "layer_idx")
+           "use_fused", "layer_idx", "dense_residuals")
 
 
 def _layer_info(c) -> dict:
@@ -120,11 +122,19 @@ def save_prompt_cache(file_name: str, cache: list, metadata: dict | None = None,
     info = [_layer_info(c) for c in cache]
     for i, c in enumerate(cache):
         state = c.state
-        packed = _dense_bits(c) if dense and isinstance(c, ChronoQuantCache) and state else {}
+        is_cq = isinstance(c, ChronoQuantCache) and bool(state)
+        packed = _dense_bits(c) if dense and is_cq else {}
+        # components whose rows are dense in HBM (dense_residuals caches)
+        in_hbm = {j: b for j, b in (_dense_bits(c) if is_cq and c.dense_residuals else {}).items()}
         for j, t in enumerate(state):
-            if j in packed:
-                t = dense_pack(t.detach().contiguous(), c.head_dim, packed[j])
-            tensors[f"{i}.{j}"] = t.detach().contiguous().cpu()
+            t = t.detach().contiguous()
+            if j in in_hbm:
+                nbytes = (c.head_dim * in_hbm[j] + 7) // 8
+                stream = t.view(torch.uint8)[..., :nbytes]  # the rows are this stream
+                t = stream if j in packed else dense_unpack(stream, c.head_dim, in_hbm[j])
+            elif j in packed:
+                t = dense_pack(t, c.head_dim, packed[j])
+            tensors[f"{i}.{j}"] = t.contiguous().cpu()
         if packed:
             info[i]["dense"] = {"head_dim": int(c.head_dim),
                                 "bits": {str(j): b for j, b in packed.items()}}

@@ -19,6 +19,14 @@
  *   packed     uint32 [B][H][cap_pframes][W]       W = ceil(D/8); nibble i of word w
  *                                                  holds code(dim 8w+i) + 8, bits 4i..4i+3
  *   scales     fp16   [B][H][cap_pframes]          one scale per P-frame row
+ * Opt-in dense rows (cq_component.packing = CQ_PACK_DENSE): a 2- or 3-bit
+ * component's packed rows hold its codes at their own width instead, as a
+ * little-endian bit stream: dim d's field code + 2^(bits-1) occupies stream
+ * bits [bits*d, bits*d + bits) (bit k of the stream is bit k % 32 of word
+ * k / 32), W = ceil(D * bits / 32) words per row, unused bits 0.  (With
+ * bits = 4 this is exactly the INT4 layout.)  This library's format: the
+ * reference has no counterpart (it names physical variable-bit packing as
+ * what its INT4 lanes are not, README.md:57, patch.py:94-98).
  * Token t of a sequence is an I-frame iff t % stride == 0; otherwise it is
  * P-frame slot t - t/stride - 1 coded against anchor t/stride.
  * The active prefix of each array is exactly the reference's tensor
@@ -62,10 +70,13 @@ typedef struct cq_component {
   int64_t cap_keyframes; /* rows reserved per (b, h) */
   int64_t cap_pframes;   /* rows reserved per (b, h) */
   int32_t stride;        /* I-frame period, >= 1 */
-  int32_t delta_bits;    /* residual bits, 2..4 (codes live in INT4 lanes) */
+  int32_t delta_bits;    /* residual bits, 2..4 */
   float dead_zone;       /* dead-zone ratio, >= 0 */
-  int32_t reserved;
+  int32_t packing;       /* CQ_PACK_INT4 (codes in INT4 lanes, the reference's
+                            layout) or CQ_PACK_DENSE (fields of delta_bits) */
 } cq_component;
+
+enum cq_packing { CQ_PACK_INT4 = 0, CQ_PACK_DENSE = 1 };
 
 typedef struct cq_cache_desc {
   int32_t batch;      /* B */

@@ -46,7 +46,8 @@ def _written(cache, b, T):
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
 @pytest.mark.parametrize("device_pos", [False, True])
-def test_fused_append_matches_two_steps(dtype, device_pos):
+@pytest.mark.parametrize("dense", [False, True])  # the 3-bit V rows stored dense
+def test_fused_append_matches_two_steps(dtype, device_pos, dense):
     from chronoquant_mlx_amd import ChronoQuantCache
     from chronoquant_mlx_amd.models import fused
     B, H, G, D, T0, steps = 3, 2, 4, 128, 13, 19
@@ -56,7 +57,8 @@ def test_fused_append_matches_two_steps(dtype, device_pos):
     qw = (1 + 0.1 * torch.randn(D, device="cuda", generator=g)).to(dtype)
     kw = (1 + 0.1 * torch.randn(D, device="cuda", generator=g)).to(dtype)
     ref, fus = [ChronoQuantCache(stride_k=4, stride_v=8, delta_bits_k=4, delta_bits_v=3,
-                                 dead_zone_k=0.0, dead_zone_v=0.05) for _ in range(2)]
+                                 dead_zone_k=0.0, dead_zone_v=0.05, dense_residuals=dense)
+                for _ in range(2)]
     k0 = torch.randn(B, H, T0, D, device="cuda", generator=g).to(dtype)
     v0 = torch.randn(B, H, T0, D, device="cuda", generator=g).to(dtype)
     for c in (ref, fus):
