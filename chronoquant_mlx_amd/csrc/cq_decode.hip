@@ -481,6 +481,16 @@ int cq_fp16_decode_attn(const uint16_t *k, const uint16_t *v, int64_t cap_tokens
     comp[i]->dead_zone = 0.f;
     comp[i]->packing = CQ_PACK_INT4;
   }
+  int st = validate_cache(&c);
+  if (st) return st;
+  DecodeArgs a;
+  st = fill_decode_args(a, &c, q, q_dtype, n_q_heads, scale, seq_lens, seq_len, max_seq_len, out,
+                        out_dtype);
+  if (st) return st;
+  // the purpose-built fp16 kernel where it applies (head_dim 128, GQA <= 4,
+  // fp16 queries), else the compressed-cache kernels over stride-1 components
+  if (fp16_g4_supported(a))
+    return launch_decode_fp16_g4(a, workspace, workspace_bytes, (hipStream_t)stream);
   return decode_entry(&c, q, q_dtype, n_q_heads, scale, seq_lens, seq_len, max_seq_len, out,
                       out_dtype, workspace, workspace_bytes, stream, true);
 }

@@ -375,7 +375,8 @@ struct SplitPlan {
 // the current device: CUs x maximum active blocks per CU, cached per device
 // under `slot` (one slot per decode kernel).
 enum ResidentSlot {
-  kSlotGeneric = 0, kSlotMfmaPow2, kSlotMfma, kSlotPlain, kSlotG4, kSlotPrefill, kSlotCount
+  kSlotGeneric = 0, kSlotMfmaPow2, kSlotMfma, kSlotPlain, kSlotG4, kSlotPrefill, kSlotFp16G4,
+  kSlotCount
 };
 int64_t resident_workgroups(const void *kernel, int threads, int slot);
 int64_t mfma_max_resident();     // max over the MFMA-file kernels
@@ -519,5 +520,9 @@ bool g4_shape(const DecodeArgs &a);
 bool g4_supported(const DecodeArgs &a);
 int64_t g4_resident();
 int launch_decode_g4(DecodeArgs &a, void *workspace, size_t ws_bytes, hipStream_t stream);
+// the uncompressed fp16 baseline at head_dim 128, GQA <= 4, fp16 queries
+bool fp16_g4_supported(const DecodeArgs &a);
+int64_t fp16_g4_resident();
+int launch_decode_fp16_g4(DecodeArgs &a, void *workspace, size_t ws_bytes, hipStream_t stream);
 
 }  // namespace cq

@@ -1054,6 +1054,153 @@ __global__ __launch_bounds__(kThreadsMfma) void decode_g4_kernel(DecodeArgs a) {
 }
 
 // ---------------------------------------------------------------------------
+// Uncompressed fp16 flash decode (cq_fp16_decode_attn), head_dim 128, GQA
+// groups of at most 4 q heads: the baseline the compressed path is measured
+// against.  K, V: fp16 [B][H][cap][128].  Same grid plan, workgroup merge and
+// split fold as decode_g4_kernel; each wave takes 64-token chunks.
+//
+// Scores: S = K q'^T with v_mfma_f32_16x16x32_f16, A = 16 K rows (token i of
+// tile j) x 32 dims, B = q' (column c = head c % 4, so every quad of lanes
+// holds the 4 heads).  K-step s covers dims 32 s .. 32 s + 31, lane group kg
+// dims 32 s + 8 kg .. + 7: one load instruction reads 64 contiguous bytes of
+// each of 16 rows (the next step the other half of their 128-byte lines, so
+// these loads keep the default cache policy and the second half hits L2).
+// P.V: A = p (rows = heads), B = V with column n of tile m = dim 8 n + m: lane
+// (n, kg) loads 16 bytes (dims 8n .. 8n + 7) of 8 token rows per 32-token
+// step (the 16 lanes of a row read it whole), and one byte permute per two
+// tokens moves element m of two rows into one operand dword.
+// ---------------------------------------------------------------------------
+struct alignas(16) F16Lds {
+  h8_t q[kG4][16];         // q' of head h, dims 8m .. 8m + 7 (heads >= G: 0)
+  uint2 p[kWaves][kG4][4][4];  // fp16 p of (wave, head, tile, lane group kg): 4 tokens
+  G4Merge mg;
+};
+
+__global__ __launch_bounds__(kThreadsMfma) void decode_fp16_g4_kernel(DecodeArgs a) {
+  __shared__ F16Lds lds;
+  prefetch_args();
+  const int split = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int col = lane & 15, kg = lane >> 4, hq = col & 3;
+  const int gn = a.G;
+  const int64_t T = seq_len_of(a, b);
+  const int64_t t0 = (int64_t)split * a.split_len, t1 = min(T, t0 + a.split_len);
+  if (split_is_empty(split, t0, T)) return;
+  const int64_t bh = (int64_t)b * a.H + h;
+  const __amdgpu_buffer_rsrc_t rk =
+      make_rsrc(a.kf[0] + bh * a.cap_kf[0] * kD, (uint32_t)(a.cap_kf[0] * kD * 2));
+  const __amdgpu_buffer_rsrc_t rv =
+      make_rsrc(a.kf[1] + bh * a.cap_kf[1] * kD, (uint32_t)(a.cap_kf[1] * kD * 2));
+
+  uint4 q_raw = uint4{0u, 0u, 0u, 0u};
+  if (tid < 64 && (tid >> 4) < gn)
+    q_raw = *(const uint4 *)((const uint16_t *)a.q +
+                             ((int64_t)b * a.nq + h * a.G + (tid >> 4)) * kD + 8 * (tid & 15));
+  uint4 kr[4][4], vr[2][8];
+  // chunk at c0 (rows past the buffer read 0; tokens past t1 are masked)
+  auto load = [&](int64_t c0) {
+    const uint32_t r0 = (uint32_t)c0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int st = 0; st < 4; ++st)
+        kr[j][st] = bload128_cached(rk, (r0 + 16u * j + col) * 256u + 64u * st + 16u * kg);
+#pragma unroll
+    for (int st = 0; st < 2; ++st)
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        vr[st][e] = bload128(rv, (r0 + 32u * st + 8u * kg + e) * 256u + 16u * col);
+  };
+  int64_t c0 = t0 + (int64_t)wave * kChunk;
+  load(c0);
+  if (tid < 64) {
+    h8_t v = {};
+    if ((tid >> 4) < gn) v = __builtin_bit_cast(h8_t, q_raw) * (_Float16)a.scale;
+    lds.q[tid >> 4][tid & 15] = v;
+  }
+  __syncthreads();
+  h8_t qb[4];
+#pragma unroll
+  for (int st = 0; st < 4; ++st) qb[st] = lds.q[hq][4 * st + kg];
+
+  float m_run = -INFINITY, l_run = 0.f;
+  f4_t acc[8];
+#pragma unroll
+  for (int nb = 0; nb < 8; ++nb) acc[nb] = f4_t{0.f, 0.f, 0.f, 0.f};
+  const h2_t ones = {(_Float16)1.f, (_Float16)1.f};
+  while (c0 < t1) {  // wave-uniform
+    const int nt = (int)min((int64_t)kChunk, t1 - c0);
+    f4_t S[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      S[j] = f4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int st = 0; st < 4; ++st) S[j] = mfma32(__builtin_bit_cast(h8_t, kr[j][st]), qb[st], S[j]);
+    }
+    // lane (col, kg): tokens 16 j + 4 kg + r of head hq, log2 units
+    float sc[4][4];
+    float mx = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        sc[j][r] = (16 * j + 4 * kg + r < nt) ? S[j][r] * kLog2e : -INFINITY;
+        mx = max_nn(mx, sc[j][r]);
+      }
+    const float cm = xor32_max(xor16_max(mx));  // the chunk's max of head hq
+    if (__any(m_run == -INFINITY || cm > m_run + kTau)) {
+      const float m_new = fmaxf(m_run, cm);
+      const float f = (m_run == -INFINITY) ? 0.f : fast_exp2(m_run - m_new);
+      l_run *= f;
+      const float fr[4] = {dpp_f<kDppQuadBcast<0>>(f), dpp_f<kDppQuadBcast<1>>(f),
+                           dpp_f<kDppQuadBcast<2>>(f), dpp_f<kDppQuadBcast<3>>(f)};
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+#pragma unroll
+        for (int nb = 0; nb < 8; ++nb) acc[nb][r] *= fr[r];
+      m_run = m_new;
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const h2_t p01 = h2_t{(_Float16)fast_exp2(sc[j][0] - m_run), (_Float16)fast_exp2(sc[j][1] - m_run)};
+      const h2_t p23 = h2_t{(_Float16)fast_exp2(sc[j][2] - m_run), (_Float16)fast_exp2(sc[j][3] - m_run)};
+      l_run = __builtin_amdgcn_fdot2(p01, ones, l_run, false);
+      l_run = __builtin_amdgcn_fdot2(p23, ones, l_run, false);
+      if (col < kG4)
+        lds.p[wave][col][j][kg] = uint2{__builtin_bit_cast(uint32_t, p01), __builtin_bit_cast(uint32_t, p23)};
+    }
+    wave_lds_sync();
+    // P.V: step st covers tokens 32 st .. + 31; A row i (head i % 4), K index
+    // 8 kg + e = token 32 st + 8 kg + e = tile 2 st + kg / 2, row 8 (kg & 1) + e
+#pragma unroll
+    for (int st = 0; st < 2; ++st) {
+      const uint4 pa = *(const uint4 *)&lds.p[wave][hq][2 * st + (kg >> 1)][2 * (kg & 1)];
+      const h8_t ap = __builtin_bit_cast(h8_t, pa);
+#pragma unroll
+      for (int m = 0; m < 4; ++m) {
+        uint32_t lo[4], hi[4];
+#pragma unroll
+        for (int e2 = 0; e2 < 4; ++e2) {
+          const uint32_t w0 = (&vr[st][2 * e2].x)[m], w1 = (&vr[st][2 * e2 + 1].x)[m];
+          lo[e2] = __builtin_amdgcn_perm(w1, w0, 0x05040100u);
+          hi[e2] = __builtin_amdgcn_perm(w1, w0, 0x07060302u);
+        }
+        acc[2 * m] = mfma32(ap, h8_of(lo[0], lo[1], lo[2], lo[3]), acc[2 * m]);
+        acc[2 * m + 1] = mfma32(ap, h8_of(hi[0], hi[1], hi[2], hi[3]), acc[2 * m + 1]);
+      }
+    }
+    wave_lds_sync();  // this chunk's p reads before the next chunk's writes
+    c0 += (int64_t)kWaves * kChunk;
+    if (c0 < t1) load(c0);
+  }
+  // head hq's weight sum: its lanes col, col + 16, col + 32, col + 48
+  l_run = xor32_sum(xor16_sum(l_run));
+  merge_finish_g4(a, lds.mg, b, h, gn, split, kGridLive, m_run, l_run,
+                  [&](int nb, int r) { return acc[nb][r]; });
+}
+
+// ---------------------------------------------------------------------------
 // host side
 // ---------------------------------------------------------------------------
 bool g4_shape(const DecodeArgs &a) {
@@ -1120,6 +1267,36 @@ int launch_decode_g4(DecodeArgs &a, void *workspace, size_t ws_bytes, hipStream_
     else
       decode_g4_kernel<false><<<grid, dim3(kThreadsMfma), 0, stream>>>(a);
   }
+  return hipGetLastError() == hipSuccess ? CQ_OK : CQ_ERR_LAUNCH;
+}
+
+bool fp16_g4_supported(const DecodeArgs &a) {
+  return a.D == kD && a.G <= kG4 && a.q_dtype == CQ_F16 && a.max_T < (1 << 24) &&
+         a.cap_kf[0] * kD * 2 < ((int64_t)1 << 31) && a.cap_kf[1] * kD * 2 < ((int64_t)1 << 31) &&
+         (((uintptr_t)a.kf[0] | (uintptr_t)a.kf[1] | (uintptr_t)a.q) & 15u) == 0;
+}
+
+int64_t fp16_g4_resident() {
+  return resident_workgroups(reinterpret_cast<const void *>(decode_fp16_g4_kernel), kThreadsMfma,
+                             kSlotFp16G4);
+}
+
+// Grid plan of one resident generation, fold records when the split slots
+// fit them (as launch_decode_g4's grid plan).
+int launch_decode_fp16_g4(DecodeArgs &a, void *workspace, size_t ws_bytes, hipStream_t stream) {
+  a.chunk_heads = kG4;
+  a.n_chunks = 1;
+  const int64_t resident = fp16_g4_resident();
+  const SplitPlan g = plan_splits((int64_t)a.B * a.H, a.max_T, resident);
+  a.nsplit = g.nsplit;
+  a.split_len = g.split_len;
+  int st = setup_workspace(a, workspace, ws_bytes);
+  if (st) return st;
+  const int64_t slots = (int64_t)a.B * a.H * a.nsplit;
+  if (a.nsplit > 1 && a.nsplit <= 64 && slots <= kMaxRecSplits && slots <= resident)
+    a.recs = records_of(workspace);
+  const dim3 grid((unsigned)a.nsplit, (unsigned)a.H, (unsigned)a.B);
+  decode_fp16_g4_kernel<<<grid, dim3(kThreadsMfma), 0, stream>>>(a);
   return hipGetLastError() == hipSuccess ? CQ_OK : CQ_ERR_LAUNCH;
 }
 

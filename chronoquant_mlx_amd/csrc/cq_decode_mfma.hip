@@ -629,7 +629,7 @@ static int64_t resident_of(int slot) {
 }
 
 int64_t mfma_max_resident() {
-  return std::max(std::max(resident_of(kSlotPlain), g4_resident()),
+  return std::max(std::max(std::max(resident_of(kSlotPlain), g4_resident()), fp16_g4_resident()),
                   std::max(resident_of(kSlotMfmaPow2), resident_of(kSlotMfma)));
 }
 

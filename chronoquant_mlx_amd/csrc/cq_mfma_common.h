@@ -84,6 +84,11 @@ __device__ __forceinline__ uint4 bload128(__amdgpu_buffer_rsrc_t r, uint32_t off
   const i4_t v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, kPolicyStream);
   return uint4{(uint32_t)v[0], (uint32_t)v[1], (uint32_t)v[2], (uint32_t)v[3]};
 }
+// the default cache policy (lines that a later load of the same wave reads again)
+__device__ __forceinline__ uint4 bload128_cached(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  const i4_t v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0);
+  return uint4{(uint32_t)v[0], (uint32_t)v[1], (uint32_t)v[2], (uint32_t)v[3]};
+}
 __device__ __forceinline__ uint32_t bload16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
   return (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(r, (int)off, 0, kPolicyStream);
 }

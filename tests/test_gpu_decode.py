@@ -362,24 +362,41 @@ def test_split_fold_outputs_and_short_bound_lengths(out_dtype):
                      what=f"{out_dtype} L={L} vs fused semantics")
 
 
-def test_fp16_baseline_matches_exact():
-    from chronoquant_mlx_amd import _lib
-    rng = np.random.default_rng(8)
-    B, H, T, D, G = 2, 8, 3000, 128, 4
-    k = rng.standard_normal((B, H, T, D)).astype(np.float16)
-    v = rng.standard_normal((B, H, T, D)).astype(np.float16)
-    q = rng.standard_normal((B, G * H, D)).astype(np.float16)
+@pytest.mark.parametrize("B,H,G,T,lens", [
+    (2, 8, 4, 3000, None),
+    (1, 8, 4, 16384, None),          # configs[1]'s shape, the one bench.py times
+    (3, 2, 2, 777, [1, 500, 777]),   # per-sequence lengths, a one-token sequence
+    (1, 1, 4, 65536, None),          # 128 splits: split-ready flags instead of records
+    (2, 4, 1, 1000, None),
+    (1, 2, 8, 700, None),            # GQA 8: the stride-1 compressed-cache kernels
+])
+def test_fp16_baseline_matches_exact(B, H, G, T, lens):
+    # cq_fp16_decode_attn (the uncompressed flash decode the compressed path is
+    # compared with) against binary64 attention on the same fp16 K/V
+    from chronoquant_mlx_amd import _lib, synth
+    D = 128
+    if (B, H, G, T) == (1, 8, 4, 16384):
+        k, v = synth.make_kv(synth.CONFIGS["c1"])
+        q = synth.make_q(synth.CONFIGS["c1"])
+    else:
+        rng = np.random.default_rng(8 + T)
+        k = rng.standard_normal((B, H, T, D)).astype(np.float16)
+        v = rng.standard_normal((B, H, T, D)).astype(np.float16)
+        q = rng.standard_normal((B, G * H, D)).astype(np.float16)
     kt, vt, qt = to_gpu(k), to_gpu(v), to_gpu(q)
-    out = torch.empty(B, G * H, D, dtype=torch.float16, device="cuda")
+    out = torch.full((B, G * H, D), float("nan"), dtype=torch.float16, device="cuda")
     need = _lib.load().cq_decode_workspace_size(B, H, G * H, D, T)
     ws = torch.zeros(need, dtype=torch.uint8, device="cuda")
+    lt = None if lens is None else torch.tensor(lens, dtype=torch.int32, device="cuda")
     _lib.call("cq_fp16_decode_attn", kt.data_ptr(), vt.data_ptr(), T, B, H, D, qt.data_ptr(),
-              _lib.CQ_F16, G * H, float(D ** -0.5), None, T, T, out.data_ptr(), _lib.CQ_F16,
-              ws.data_ptr(), need, _lib.stream_of(qt))
+              _lib.CQ_F16, G * H, float(D ** -0.5), _lib.ptr(lt), T, T, out.data_ptr(),
+              _lib.CQ_F16, ws.data_ptr(), need, _lib.stream_of(qt))
     got = out.float().cpu().numpy()
     for b in range(B):
-        ref = O.sdpa_exact(q[b], k[b], v[b], D ** -0.5)
+        L = T if lens is None else lens[b]
+        ref = O.sdpa_exact(q[b], k[b][:, :L], v[b][:, :L], D ** -0.5)
         assert_close(got[b], ref, what=f"fp16 baseline b={b}")
+        assert_tight(got[b], ref, what=f"fp16 baseline b={b} (binary64)")
 
 
 def test_sdpa_dispatch_and_fallback():
