@@ -103,7 +103,7 @@ def test_c4_model_layers_against_oracle():
     from chronoquant_mlx_amd import create_full_throttle_caches, patch, synth
     from chronoquant_mlx_amd.models import qwen
     args = qwen.ModelArgs()  # configs[4]: 32 layers, hidden 4096, GQA 32/8, SwiGLU 12288
-    prompt_len, chunk, n_dec = 8192, 512, 4
+    prompt_len, chunk, n_dec = 8192, 512, 12
     H, D, nq = args.num_key_value_heads, args.head_dim, args.num_attention_heads
     print("c4 model: building the full-size random model", flush=True)
     model = qwen.random_model(args, seed=0)
@@ -170,3 +170,56 @@ def test_c4_model_layers_against_oracle():
             err, rel = assert_close(got, ref, what=f"layer {i} call {c} T={Tc}")
             print(f"c4 model: layer {i} call {c} (T={Tc}) max-abs {err:.2e} rel {rel:.2e}",
                   flush=True)
+
+    # ---- the same generation with the decode steps replayed from one HIP
+    # graph (the form bench.py times): the captured step records its layer
+    # 0 / 31 queries and outputs into device buffers at the step index
+    # position - prompt_len, so each replay's are kept
+    patch.apply()
+    try:
+        caches_g = create_full_throttle_caches(model)
+        slot = {id(caches_g[i]): i for i in layers}
+        qb = {i: torch.zeros(n_dec, 1, nq, 1, D, dtype=torch.bfloat16, device="cuda")
+              for i in layers}
+        ob = {i: torch.zeros_like(qb[i]) for i in layers}
+
+        def sdpa_g(queries, keys, values, cache, scale, mask=None, **kw):
+            out = patched(queries, keys, values, cache=cache, scale=scale, mask=mask, **kw)
+            i = slot.get(id(cache))
+            if i is not None and cache._dev_pos is not None:  # a decode step
+                idx = (cache._dev_pos[:1].long() - prompt_len).clamp(0, n_dec - 1)
+                qb[i].index_copy_(0, idx, queries.detach()[None])
+                ob[i].index_copy_(0, idx, out.detach()[None])
+            return out
+
+        qwen.scaled_dot_product_attention = sdpa_g
+        toks_g, _, _ = qwen.generate(model, caches_g, prompt, n_dec + 1, prefill_chunk=chunk,
+                                     graph=True)
+    finally:
+        patch.revert()
+    torch.cuda.synchronize()
+    print(f"c4 model: graph-captured decode of {n_dec} steps done", flush=True)
+    assert torch.equal(toks_g, toks), "graph decode chose other tokens than eager decode"
+    # every layer's cache after the graph replays equals the eager run's
+    for li, (cg, ce) in enumerate(zip(caches_g, caches)):
+        assert cg.offset == ce.offset == T
+        for x, y in zip(cg.state, ce.state):
+            assert torch.equal(x.view(torch.int16) if x.dtype != torch.uint32 else x,
+                               y.view(torch.int16) if y.dtype != torch.uint32 else y), \
+                f"layer {li}: graph-decoded cache state differs"
+    for i in layers:
+        r = recs[i]  # the eager run's K/V: the same bits (states are equal)
+        ck = O.OracleComponent(H, D, 64, 4, 0.0, capacity=T)
+        cv = O.OracleComponent(H, D, 32, 3, 0.05, capacity=T)
+        ck.append(_bf16_bits(torch.cat(r.k, dim=2))[0], "bf16")
+        cv.append(_bf16_bits(torch.cat(r.v, dim=2))[0], "bf16")
+        rk, rv = ck.reconstruct(), cv.reconstruct()
+        for sidx in range(n_dec):
+            Tc = prompt_len + sidx + 1
+            q = qb[i][sidx, 0, :]  # [nq, 1, D]
+            assert torch.equal(q.view(torch.int16), r.q[n_pre + sidx][0].view(torch.int16)), \
+                f"layer {i} graph step {sidx}: query differs from the eager step's"
+            ref = _bf16_fallback(q, rk[:, :Tc], rv[:, :Tc], scale, causal=False)
+            got = ob[i][sidx, 0].float().cpu().numpy()
+            err, rel = assert_close(got, ref, what=f"layer {i} graph step {sidx} T={Tc}")
+        print(f"c4 model: layer {i} graph steps vs oracle ok (last max-abs {err:.2e})", flush=True)

@@ -35,7 +35,7 @@ def test_c3_streaming_graph():
     from chronoquant_mlx_amd import ChronoQuantCache, _lib, synth
     cfg = synth.CONFIGS["c3"]
     B, H, D, nq = cfg.B, cfg.n_kv_heads, cfg.head_dim, cfg.n_q_heads
-    steps = 2 * max(cfg.stride_k, cfg.stride_v)  # every sequence crosses K and V I-frames
+    steps = 256  # the loop bench.py times: 256 steps (every sequence crosses I-frames)
     lens = cfg.lengths()
     t_max = int(lens.max())
     cap = t_max + steps
@@ -121,14 +121,14 @@ def test_c3_streaming_graph():
             assert np.array_equal(g_pk, pk), f"b={b} packed[{i}]"
             assert np.array_equal(g_sc.view(np.uint16), sc.view(np.uint16)), f"b={b} scales[{i}]"
         rk, rv = ck.reconstruct(), cv.reconstruct()
-        for s in range(steps):
+        # every 16th step (and the first and last) against the oracle
+        for s in sorted(set(range(0, steps, 16)) | {1, steps - 1}):
             T = int(lens[b]) + s + 1
             ref = _fallback_prefix(q_np[s, b], rk, rv, T, scale)
             e, _ = assert_close(out[s, b], ref, what=f"b={b} step={s} T={T}")
             worst = max(worst, e)
-            if s % 8 == 7 or s == 0:
-                assert_tight(out[s, b], O.sdpa_fused(q_np[s, b], ck, cv, scale, T=T),
-                             what=f"b={b} step={s} T={T}")
+            assert_tight(out[s, b], O.sdpa_fused(q_np[s, b], ck, cv, scale, T=T),
+                         what=f"b={b} step={s} T={T}")
     # the bar also holds as a plain max-abs (outputs reach [2, 4), where one
     # fp16 ulp is 1.95e-3)
     assert worst <= ATOL, worst
