@@ -12,7 +12,9 @@ import re
 import torch  # loads the process's HIP runtime before libchronoquant.so binds to it
 
 PKG = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(PKG, "libchronoquant.so")
+# CQ_LIBRARY selects another build of the library (phase_times.py's
+# diagnostic build); the product loads libchronoquant.so
+LIB_PATH = os.environ.get("CQ_LIBRARY") or os.path.join(PKG, "libchronoquant.so")
 HEADER = os.path.join(os.path.dirname(PKG), "include", "chronoquant.h")
 
 CQ_OK = 0

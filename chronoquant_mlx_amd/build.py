@@ -41,19 +41,26 @@ def sources() -> list[str]:
     return sorted(os.path.join(CSRC, f) for f in os.listdir(CSRC) if f.endswith(".hip"))
 
 
-def build(verbose: bool = False) -> str:
+PHASES_OUT = os.path.join(PKG, "libchronoquant_phases.so")
+
+
+def build(verbose: bool = False, phases: bool = False) -> str:
+    """Build libchronoquant.so; phases=True builds the diagnostic
+    libchronoquant_phases.so instead (the decode kernels record per-workgroup
+    phase times, read by phase_times.py)."""
     hipcc = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
-    tmp = OUT + ".tmp"
-    cmd = [hipcc, *HIPCC_FLAGS, "-o", tmp, *sources()]
+    out = PHASES_OUT if phases else OUT
+    tmp = out + ".tmp"
+    cmd = [hipcc, *HIPCC_FLAGS, *(["-DCQ_PHASE_TIMES"] if phases else []), "-o", tmp, *sources()]
     if verbose:
         print(" ".join(cmd), flush=True)
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         sys.stderr.write(res.stdout + res.stderr)
         raise RuntimeError("hipcc failed building libchronoquant.so")
-    os.replace(tmp, OUT)
-    return OUT
+    os.replace(tmp, out)
+    return out
 
 
 if __name__ == "__main__":
-    print(build(verbose=True))
+    print(build(verbose=True, phases="--phases" in sys.argv[1:]))

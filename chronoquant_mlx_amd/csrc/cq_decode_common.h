@@ -71,6 +71,25 @@ __device__ __forceinline__ void prefetch_args() {
       : "s"(p));
 }
 
+#ifdef CQ_PHASE_TIMES
+// Diagnostic build only (libchronoquant_phases.so, built with
+// -DCQ_PHASE_TIMES; see phase_times.py): thread 0 of every workgroup of a
+// fold-record launch stores the device clock (s_memrealtime, 100 MHz, the
+// same on every CU) at phase p into slot [linear workgroup][p] of the
+// split-partial area, which such launches leave unused.
+// (Wave 0 stores, every lane the same value: a branch on the thread index
+// would make the compiler treat the block indices behind it as divergent
+// and wrap the kernel's buffer loads in waterfall loops.)
+__device__ __forceinline__ void phase_mark(const DecodeArgs &a, int p) {
+  if (__builtin_amdgcn_readfirstlane(threadIdx.x >> 6) == 0 && a.recs && a.part_acc) {
+    const uint32_t wg = blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z);
+    ((uint64_t *)a.part_acc)[wg * 8u + (uint32_t)p] = __builtin_amdgcn_s_memrealtime();
+  }
+}
+#else
+__device__ __forceinline__ void phase_mark(const DecodeArgs &, int) {}
+#endif
+
 __device__ __forceinline__ int64_t seq_len_of(const DecodeArgs &a, int b) {
   return a.seq_lens ? min((int64_t)max(a.seq_lens[b], 0), a.max_T) : a.seq_len;
 }

@@ -386,7 +386,9 @@ __device__ __forceinline__ void merge_finish_g4(const DecodeArgs &a, G4Merge &M,
   if (single) return;
   if (live == kGridLive) live = grid_live(a, seq_len_of(a, b));
   if (a.recs) {
+    phase_mark(a, 4);  // records stored (issued)
     fold_records_g4(a, b, h, gn, slot, live);
+    phase_mark(a, 5);  // fold done, outputs stored (issued)
     return;
   }
   if (a.flags) {
@@ -479,6 +481,7 @@ __global__ __launch_bounds__(kThreadsMfma) void decode_g4_kernel(DecodeArgs a) {
   // segment body keeps the scalar registers of a one-segment kernel.
   __shared__ int32_t s_loop[8];  // cursor unit [2], cursor sequence [2], end unit, P, n
   prefetch_args();
+  phase_mark(a, 0);  // workgroup started
   const int h = blockIdx.y;  // kv head: one q-head chunk (G <= 4)
   const bool table = kBalanced && a.seq_lens && a.B > 1 && a.B <= kMaxTableSeqs;
   if constexpr (kBalanced) {
@@ -703,6 +706,7 @@ __global__ __launch_bounds__(kThreadsMfma) void decode_g4_kernel(DecodeArgs a) {
     // stages a chunk past the end (no traffic, zeros).
     stage((int)min(c0l, t1), bufA);
     stage_va((int)min(c0l, t1));
+    phase_mark(a, 1);  // first chunk's loads issued
 
     // ---- q table: q' = fp16(q * fp16(scale)) (bf16 queries: bf16(q * bf16(scale)))
     // per (parity, slab pair, head) in the order unpack_pair gives a code
@@ -728,6 +732,7 @@ __global__ __launch_bounds__(kThreadsMfma) void decode_g4_kernel(DecodeArgs a) {
       (&Gs.zero[0][0])[tid - 64] = h8_t{};
     }
     __syncthreads();
+    phase_mark(a, 2);  // q table ready
     // score-layout B operand of (parity, pair): Gs.q[..][hq] on the diagonal blocks, else zeros
     const h8_t *qsrc = jb == kg ? &Gs.q[0][hq] : &Gs.zero[0][hq];
     // 16-head-layout B operand of the anchor product (q'^T, column = head)
@@ -997,6 +1002,7 @@ __global__ __launch_bounds__(kThreadsMfma) void decode_g4_kernel(DecodeArgs a) {
     // most one chunk per wave (kOneChunk) have nothing to pipeline.
     if constexpr (kOneChunk) {
       if (has_work) compute(bufA, 0);
+      phase_mark(a, 3);  // wave 0's chunk computed (issued)
     } else if (has_work) {
       // The wave's n >= 1 chunks c0l, c0l + kStep, ... below t1, in pairs and
       // one last single chunk, so that the loop has one exit, at its end.  (An
