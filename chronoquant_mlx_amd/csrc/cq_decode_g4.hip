@@ -74,6 +74,7 @@ struct alignas(16) G4WaveScratch : G4WaveRows<kContig> {
 // lanes read.
 struct alignas(16) G4GroupScratch {
   h8_t q[16][kG4];
+  h8_t qn[16][kG4];  // q' of head h, dims 8m .. 8m + 7 (natural order): the anchor product's B
   h8_t pad[kG4];  // puts zero[m][h] 64 bytes off q[m][h]'s banks
   h8_t zero[16][kG4];
   float s8[kG4];  // 8 * sum_d q'_d per head
@@ -426,13 +427,6 @@ __device__ __forceinline__ h8_t unpack_pair(uint32_t wa, uint32_t wb, uint32_t t
                                            uint32_t m) {
   return h8_of(wa & m, ta & m, wb & m, tb & m);
 }
-// The same dims of an anchor row (fp16, natural order) for the anchor product:
-// u = dims 0..7 of slab 2p, v = of slab 2p + 1.
-__device__ __forceinline__ h8_t anchor_pair(uint4 u, uint4 v, bool odd) {
-  const uint32_t sel = odd ? 0x07060302u : 0x05040100u;
-  return h8_of(__builtin_amdgcn_perm(u.z, u.x, sel), __builtin_amdgcn_perm(u.w, u.y, sel),
-               __builtin_amdgcn_perm(v.z, v.x, sel), __builtin_amdgcn_perm(v.w, v.y, sel));
-}
 
 // The registers one chunk's loads land in.  kr and vw first hold the chunk's
 // contiguous K and V code blocks (16 bytes of slot row base + 16q + lane / 4,
@@ -611,6 +605,13 @@ __global__ __launch_bounds__(kThreadsMfma) void decode_g4_kernel(DecodeArgs a) {
         }
       }
     }
+    // Lane constants.  Every computed chunk starts at a multiple of 64 tokens,
+    // so for a power-of-two stride 2^s and 0 <= x < 64, (c0 + x) >> s =
+    // (c0 >> s) + (x >> s), and (c0 + x) is a multiple of 2^s iff both c0 and
+    // x are: token indices within the chunk split into a uniform part and a
+    // lane constant.
+    const int lane_sk = lane - (lane >> lsk), lane_sv = lane - (lane >> lsv);
+    const bool lane_pk = (lane & mk) != 0, lane_pv = (lane & mv) != 0;
     auto stage = [&](int c0, G4Buf &cb) {
       const int nt = (int)max((int64_t)0, min((int64_t)kChunk, t1 - c0));
       cb.c0 = c0;
@@ -620,10 +621,12 @@ __global__ __launch_bounds__(kThreadsMfma) void decode_g4_kernel(DecodeArgs a) {
       // anchor offsets stay below 2^30; buffers are below 2^31 bytes (mfma_supported)
       const uint32_t dead = nt ? 0u : 0x80000000u;
       {
+        // slot t - t / stride - 1 of token t = c0 + lane (a P-frame iff t is
+        // not a multiple of the stride; a chunk without tokens reads nothing)
         const bool valid = lane < nt;
-        const int t = c0 + lane;
-        const int slk = (valid && (t & mk)) ? t - (t >> lsk) - 1 : -1;
-        const int slv = (valid && (t & mv)) ? t - (t >> lsv) - 1 : -1;
+        const bool pk = (c0 & mk) != 0 || lane_pk, pv = (c0 & mv) != 0 || lane_pv;
+        const int slk = (valid && pk) ? c0 - gk_base - 1 + lane_sk : -1;
+        const int slv = (valid && pv) ? c0 - (c0 >> lsv) - 1 + lane_sv : -1;
         // slot -1 reads past the buffer: scale 0, codes 0
         cb.sk = bload16(r_sck, (uint32_t)slk * 2u);
         cb.sv = bload16(r_scv, (uint32_t)slv * 2u);
@@ -680,11 +683,11 @@ __global__ __launch_bounds__(kThreadsMfma) void decode_g4_kernel(DecodeArgs a) {
     auto stage_va = [&](int c0) {
       const int nt = (int)max((int64_t)0, min((int64_t)kChunk, t1 - c0));
       const int gv_base = c0 >> lsv;
-      const int gv_last = nt ? (c0 + nt - 1) >> lsv : gv_base;
-      const uint32_t dead = nt ? 0u : 0x80000000u;
+      // anchors gv_base + min(4kg + r, last - gv_base), last = (c0 + nt - 1) / stride
+      const int dv = nt ? (nt - 1) >> lsv : 0;
+      const uint32_t base = (((uint32_t)gv_base * 256u) | (nt ? 0u : 0x80000000u)) + 16u * col;
 #pragma unroll
-      for (int r = 0; r < 4; ++r)
-        va[r] = bload128(r_kfv, ((uint32_t)min(gv_base + 4 * kg + r, gv_last) * 256u + 16u * col) | dead);
+      for (int r = 0; r < 4; ++r) va[r] = bload128(r_kfv, (uint32_t)min(4 * kg + r, dv) * 256u + base);
     };
 
     // Wave 0's q rows are requested first, then every wave's first chunk:
@@ -726,6 +729,7 @@ __global__ __launch_bounds__(kThreadsMfma) void decode_g4_kernel(DecodeArgs a) {
       // slab m is half m & 1 of pair m >> 1
       ((h4_t *)&Gs.q[m >> 1][hh])[m & 1] = h4_t{v[0], v[4], v[2], v[6]};
       ((h4_t *)&Gs.q[8 + (m >> 1)][hh])[m & 1] = h4_t{v[1], v[5], v[3], v[7]};
+      Gs.qn[m][hh] = v;
       part = row16_sum(part);  // the 16 lanes m of head hh
       if (m == 0) Gs.s8[hh] = 8.f * part;
     } else if (tid < 128) {
@@ -736,7 +740,17 @@ __global__ __launch_bounds__(kThreadsMfma) void decode_g4_kernel(DecodeArgs a) {
     // score-layout B operand of (parity, pair): Gs.q[..][hq] on the diagonal blocks, else zeros
     const h8_t *qsrc = jb == kg ? &Gs.q[0][hq] : &Gs.zero[0][hq];
     // 16-head-layout B operand of the anchor product (q'^T, column = head)
-    const h8_t *qcol = col < kG4 ? &Gs.q[0][col] : &Gs.zero[0][0];
+    const h8_t *qcol = col < kG4 ? &Gs.qn[0][col] : &Gs.zero[0][0];
+    // the anchor table row of this lane's score tokens 16 jb + 4 kg (+ r < 4)
+    const int qa_row = (16 * jb + 4 * kg) >> lsk;
+    // E^T operand dwords of the P_g product (group col against tokens 32P +
+    // 4kg + e and 32P + 16 + 4kg + e): fp16 1.0 pairs or zero
+    uint32_t eop[2][2];
+#pragma unroll
+    for (int P = 0; P < 2; ++P) {
+      eop[P][0] = ((32 * P + 4 * kg) >> lsv) == col ? 0x3c003c00u : 0u;
+      eop[P][1] = ((32 * P + 16 + 4 * kg) >> lsv) == col ? 0x3c003c00u : 0u;
+    }
     const float s8l = Gs.s8[hq] * kLog2e;
 
     uint32_t magic;  // fp16 1024 in both halves, held in a VGPR for v_and_or_b32
@@ -806,9 +820,9 @@ __global__ __launch_bounds__(kThreadsMfma) void decode_g4_kernel(DecodeArgs a) {
         f4_t d = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         // product kb: lane group kg supplies parity kb & 1 of slabs 4kg + 2(kb >> 1), +1
+        // product kb: lane group kg supplies dims 32kg + 8kb .. + 7 (natural order)
         for (int kb = 0; kb < 4; ++kb)
-          d = mfma32(anchor_pair(cb.ka[kb & 2], cb.ka[(kb & 2) + 1], kb & 1),
-                     qcol[(8 * (kb & 1) + 2 * kg + (kb >> 1)) * kG4], d);
+          d = mfma32(__builtin_bit_cast(h8_t, cb.ka[kb]), qcol[(4 * kg + kb) * kG4], d);
         if (col < kG4) {
           const float mref = (m_run == -INFINITY) ? 0.f : m_run;
 #pragma unroll
@@ -839,7 +853,7 @@ __global__ __launch_bounds__(kThreadsMfma) void decode_g4_kernel(DecodeArgs a) {
       const uint4 s4 = *(const uint4 *)&W.s16[sl][tb];
       const uint32_t sr[4] = {s4.x, s4.y, s4.z, s4.w};
       // the 4 tokens share one K anchor (stride >= 4, token groups aligned to 4)
-      const float qa = W.qa[((c0 + tb) >> lsk) - gk_base][hq];
+      const float qa = W.qa[qa_row][hq];
       float sc[4];
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
@@ -922,10 +936,7 @@ __global__ __launch_bounds__(kThreadsMfma) void decode_g4_kernel(DecodeArgs a) {
         const h8_t aw = h8_of(wa.x, wa.y, wb.x, wb.y);
         // E^T: group col x these tokens (fp16 1.0 = 0x3c00); each run of 4
         // tokens lies in one V group (stride >= 4)
-        const int ga = ((c0 + 32 * P + 4 * kg) >> lsv) - gv_base;
-        const int gb = ((c0 + 32 * P + 16 + 4 * kg) >> lsv) - gv_base;
-        const uint32_t ea = ga == col ? 0x3c003c00u : 0u, eb = gb == col ? 0x3c003c00u : 0u;
-        pg = mfma32(h8_of(ea, ea, eb, eb), ap, pg);
+        pg = mfma32(h8_of(eop[P][0], eop[P][0], eop[P][1], eop[P][1]), ap, pg);
         const int i0 = 2 * P, i1 = 2 * P + 1;
         if constexpr (kDenseV) {
           // V codes, dense rows: B = 8 tokens x dim 8col + e.  Byte pairs of
