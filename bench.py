@@ -532,17 +532,20 @@ def cpu_threads() -> tuple[int, str]:
     return aff, f"all {aff} CPUs in the process affinity"
 
 
-def cpu_baseline_config(cfg, k, v, q, threads, runs=20, warmup=3, max_s=15.0):
-    """The reference's per-layer decode work, restated in C (oracle/): one
+def cpu_baseline_config(cfg, k, v, q, threads, runs=50, warmup=3, max_s=10.0, fallback_runs=3):
+    """The reference's per-layer decode work on the host CPU (oracle/): one
     token's append (codec + INT4 pack + I-frame, cache.py:87-129 with
-    codec.py:23-65 and kernels.py:34-54) and the attention (reconstruct K/V,
-    cache.py:131-160, then the fallback SDPA, attention.py:61-74), timed
-    separately: median of `runs` after `warmup` (fewer runs if max_s runs
-    out)."""
+    codec.py:23-65 and kernels.py:34-54) and the fused compressed-cache
+    attention of kernels.py:79-228 in fp32 (oracle/cq_cpu_baseline.c:
+    OpenMP over kv-head x key-chunk tasks, AVX2), over the same T tokens the
+    GPU decodes; medians of `runs` after `warmup` (fewer if max_s runs
+    out).  Also times, `fallback_runs` times, the reference's other decode
+    route: reconstruct K/V (cache.py:131-160) and the fallback SDPA
+    (attention.py:61-74), the oracle's binary64-accumulating restatement."""
     from oracle import oracle as O
     O.set_threads(threads)
     H, D, T = cfg.n_kv_heads, cfg.head_dim, cfg.T
-    n_app = runs + warmup
+    n_app = 23
     ck = O.OracleComponent(H, D, cfg.stride_k, cfg.delta_bits_k, cfg.dead_zone_k,
                            capacity=T + n_app)
     cv = O.OracleComponent(H, D, cfg.stride_v, cfg.delta_bits_v, cfg.dead_zone_v,
@@ -559,24 +562,33 @@ def cpu_baseline_config(cfg, k, v, q, threads, runs=20, warmup=3, max_s=15.0):
         ck.append(tok)
         cv.append(vtok)
         t_app.append(time.perf_counter() - t0)
-    t_app = t_app[warmup:]
-    Tn = ck.offset
-    scratch = (np.empty((H, Tn, D), np.uint16), np.empty((H, Tn, D), np.uint16))
+    t_app = t_app[3:]
     t_att = []
     out = None
     t_start = time.perf_counter()
-    for i in range(n_app):
+    for i in range(runs + warmup):
         t0 = time.perf_counter()
-        out = O.decode_step(q[0], ck, cv, D ** -0.5, scratch)
+        out = O.fused_decode_f32(q[0], ck, cv, D ** -0.5, T=T)
         if i >= warmup:
             t_att.append(time.perf_counter() - t0)
         if time.perf_counter() - t_start > max_s and len(t_att) >= 5:
             break
-    return float(np.median(t_app)), float(np.median(t_att)), len(t_att), Tn, out
+    t_fb = []
+    if fallback_runs:
+        Tn = ck.offset
+        scratch = (np.empty((H, Tn, D), np.uint16), np.empty((H, Tn, D), np.uint16))
+        O.decode_step(q[0], ck, cv, D ** -0.5, scratch)
+        for i in range(fallback_runs):
+            t0 = time.perf_counter()
+            O.decode_step(q[0], ck, cv, D ** -0.5, scratch)
+            t_fb.append(time.perf_counter() - t0)
+    return (float(np.median(t_app)), float(np.median(t_att)), len(t_att), out,
+            float(np.median(t_fb)) if t_fb else None)
 
 
 def cpu_baseline(q_np_c1, ref_c1, algo_c1):
-    """cpu_baseline for the JSON line: c1 (the metric's workload) and c0."""
+    """cpu_baseline for the JSON line: c1 (the metric's workload) and c0.
+    ref_c1: the GPU's c1 output (fp32 [nq, D]) to compare with, or None."""
     from chronoquant_mlx_amd import synth
     threads, why = cpu_threads()
     res = {}
@@ -584,24 +596,29 @@ def cpu_baseline(q_np_c1, ref_c1, algo_c1):
         cfg = synth.CONFIGS[name]
         k, v = synth.make_kv(cfg)
         q = q_np_c1 if name == "c1" else synth.make_q(cfg)
-        t_app, t_att, n, Tn, out = cpu_baseline_config(cfg, k, v, q, threads)
+        t_app, t_att, n, out, t_fb = cpu_baseline_config(cfg, k, v, q, threads)
         algo = synth.algorithmic_decode_bytes(cfg)
         res[name] = {"append_us": round(t_app * 1e6, 2), "attention_us": round(t_att * 1e6, 1),
                      "step_us": round((t_app + t_att) * 1e6, 1),
                      "GBps": round(algo / (t_app + t_att) / 1e9, 3), "runs": n,
-                     "context": Tn}
-        log(f"[bench] CPU {name}: append {t_app * 1e6:.1f} us + attention {t_att * 1e6:.0f} us "
-            f"on {threads} threads")
+                     "context": cfg.T,
+                     "fallback_attention_us": None if t_fb is None else round(t_fb * 1e6, 1)}
+        log(f"[bench] CPU {name}: append {t_app * 1e6:.1f} us + fused attention "
+            f"{t_att * 1e6:.0f} us on {threads} threads (reconstruct + fallback SDPA "
+            f"{(t_fb or 0) * 1e6:.0f} us)")
         if name == "c1" and ref_c1 is not None:
             res[name]["gpu_vs_cpu_max_abs_diff"] = float(
                 np.abs(ref_c1.astype(np.float32) - out.astype(np.float32)).max())
     c1 = res["c1"]
     return {"value": c1["GBps"], "unit": "GB/s", "cores": threads, "kind": "port",
             "cpu_model": cpu_model(), "threads_rule": why,
-            "sample": "the reference's per-layer decode step restated in C (oracle/cq_oracle.c): "
-                      "append of one token (codec + pack) and attention (reconstruct K/V + "
-                      f"fallback SDPA) over the full c1 / c0 cache, medians of >= 20 runs after "
-                      f"3 warm-ups; value = c1 algorithmic bytes ({algo_c1}) / (append + attention)",
+            "sample": "the reference's per-layer decode step on the host CPU (oracle/): append of "
+                      "one token (codec + pack, oracle/cq_oracle.c) and the fused compressed-cache "
+                      "attention of kernels.py:79-228 in fp32 (oracle/cq_cpu_baseline.c: OpenMP "
+                      "kv-head x key-chunk tasks, AVX2/F16C) over the full c1 / c0 cache, medians "
+                      f"of up to 50 runs after 3 warm-ups; value = c1 algorithmic bytes ({algo_c1}) "
+                      "/ (append + attention).  fallback_attention_us: reconstruct K/V + fallback "
+                      "SDPA (binary64 sums), the reference's unfused route, 3 runs",
             "configs": res}
 
 
@@ -770,10 +787,8 @@ def main():
         result["extra"] = extra
 
     if not args.no_cpu_baseline and cfg.name == "c1":
-        log("[bench] CPU baseline (oracle restatement of append + reconstruct + fallback SDPA)")
-        # the CPU sample appends tokens after the timed cache state, so its
-        # attention runs over a slightly longer context than the GPU's
-        result["cpu_baseline"] = cpu_baseline(q_np, None, algo_bytes)
+        log("[bench] CPU baseline (append + fused fp32 attention on the host CPU)")
+        result["cpu_baseline"] = cpu_baseline(q_np, ref[0].float().cpu().numpy(), algo_bytes)
 
     print(json.dumps(result), flush=True)
 

@@ -57,6 +57,9 @@ def lib() -> ctypes.CDLL:
         L.cqo_num_keyframes.restype = I64
         L.cqo_num_pframes.argtypes = [I64, I32]
         L.cqo_num_pframes.restype = I64
+        L.cqb_fused_decode_f32.argtypes = [P, I32, I32, I32, I64, F, I32, I32,
+                                           P, I64, P, I64, P, P, I64, P, I64, P, I32, P]
+        L.cqb_fused_decode_f32.restype = I32
         _lib = L
     return _lib
 
@@ -245,6 +248,25 @@ def sdpa_fused(q: np.ndarray, ck: OracleComponent, cv: OracleComponent,
                               _p(ck.sc), _p(cv.kf), cv.cap_kf, _p(cv.pk), cv.cap_pf,
                               _p(cv.sc), _p(out), None if absw is None else _p(absw))
     return (out, absw) if return_absw else out
+
+
+def fused_decode_f32(q: np.ndarray, ck: OracleComponent, cv: OracleComponent,
+                     scale: float, T: int | None = None, n_chunks: int = 0) -> np.ndarray:
+    """CPU baseline (oracle/cq_cpu_baseline.c) of the fused operator
+    kernels.py:79-228 in fp32: blockwise online softmax over key chunks on
+    OpenMP threads.  q fp16 [nq, D] -> fp32 [nq, D]."""
+    q = np.ascontiguousarray(q, np.float16).view(np.uint16)
+    nq, D = q.shape
+    T = ck.offset if T is None else int(T)
+    assert 0 <= T <= min(ck.offset, cv.offset)
+    out = np.empty((nq, D), np.float32)
+    rc = lib().cqb_fused_decode_f32(_p(q), nq, ck.H, D, T, float(scale), ck.stride,
+                                    cv.stride, _p(ck.kf), ck.cap_kf, _p(ck.pk), ck.cap_pf,
+                                    _p(ck.sc), _p(cv.kf), cv.cap_kf, _p(cv.pk), cv.cap_pf,
+                                    _p(cv.sc), int(n_chunks), _p(out))
+    if rc != 0:
+        raise ValueError("shape outside the CPU baseline's vectorised form")
+    return out
 
 
 def sdpa_exact(q: np.ndarray, k: np.ndarray, v: np.ndarray, scale: float) -> np.ndarray:
