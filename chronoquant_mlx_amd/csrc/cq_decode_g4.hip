@@ -1096,6 +1096,7 @@ struct alignas(16) F16Lds {
 __global__ __launch_bounds__(kThreadsMfma) void decode_fp16_g4_kernel(DecodeArgs a) {
   __shared__ F16Lds lds;
   prefetch_args();
+  phase_mark(a, 0);  // workgroup started
   const int split = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -1131,12 +1132,14 @@ __global__ __launch_bounds__(kThreadsMfma) void decode_fp16_g4_kernel(DecodeArgs
   };
   int64_t c0 = t0 + (int64_t)wave * kChunk;
   load(c0);
+  phase_mark(a, 1);  // first chunk's loads issued
   if (tid < 64) {
     h8_t v = {};
     if ((tid >> 4) < gn) v = __builtin_bit_cast(h8_t, q_raw) * (_Float16)a.scale;
     lds.q[tid >> 4][tid & 15] = v;
   }
   __syncthreads();
+  phase_mark(a, 2);  // q table ready
   h8_t qb[4];
 #pragma unroll
   for (int st = 0; st < 4; ++st) qb[st] = lds.q[hq][4 * st + kg];
@@ -1211,6 +1214,7 @@ __global__ __launch_bounds__(kThreadsMfma) void decode_fp16_g4_kernel(DecodeArgs
     c0 += (int64_t)kWaves * kChunk;
     if (c0 < t1) load(c0);
   }
+  phase_mark(a, 3);  // wave 0's chunks computed (issued)
   // head hq's weight sum: its lanes col, col + 16, col + 32, col + 48
   l_run = xor32_sum(xor16_sum(l_run));
   merge_finish_g4(a, lds.mg, b, h, gn, split, kGridLive, m_run, l_run,

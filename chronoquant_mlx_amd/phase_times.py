@@ -1,7 +1,7 @@
 """Where the time of one B=1 fused decode goes (diagnostic).
 
     python -m chronoquant_mlx_amd.build --phases
-    python -m chronoquant_mlx_amd.phase_times [--config c1] [--launches 200]
+    python -m chronoquant_mlx_amd.phase_times [--config c1] [--launches 200] [--fp16]
 
 Runs the decode of a benchmark configuration with libchronoquant_phases.so,
 the library built with -DCQ_PHASE_TIMES: wave 0 of every workgroup of a
@@ -12,6 +12,10 @@ area:
     0 workgroup started      1 first chunk's loads issued
     2 q table ready          3 wave 0's chunk computed (one-chunk splits)
     4 fold records stored    5 fold done, outputs stored
+
+With --fp16 the launches are the uncompressed fp16 decode
+(cq_fp16_decode_attn) over the configuration's fp16 K/V, which marks the
+same points (3: wave 0's chunks computed).
 
 Each launch is timed from its earliest phase-0 stamp.  The summary gives,
 per phase, the median over launches of the median and of the latest
@@ -46,6 +50,8 @@ def main() -> None:
     ap.add_argument("--config", default="c1")
     ap.add_argument("--launches", type=int, default=200)
     ap.add_argument("--replicas", type=int, default=57)
+    ap.add_argument("--fp16", action="store_true",
+                    help="time the uncompressed fp16 decode over the same K/V")
     args = ap.parse_args()
     if not os.path.exists(PHASES_LIB):
         sys.exit(f"{PHASES_LIB} is not built: python -m chronoquant_mlx_amd.build --phases")
@@ -59,35 +65,47 @@ def main() -> None:
     cfg = synth.CONFIGS[args.config]
     dev = torch.device("cuda:0")
     k, v = synth.make_kv(cfg)
-    base = ChronoQuantCache(stride_k=cfg.stride_k, stride_v=cfg.stride_v,
-                            delta_bits_k=cfg.delta_bits_k, delta_bits_v=cfg.delta_bits_v,
-                            dead_zone_k=cfg.dead_zone_k, dead_zone_v=cfg.dead_zone_v,
-                            capacity=cfg.T)
-    base.update_and_fetch(torch.from_numpy(k).to(dev), torch.from_numpy(v).to(dev))
-    import copy
-    caches = [base]
-    for _ in range(args.replicas - 1):  # cycle replicas so bytes come from HBM
-        c = copy.copy(base)
-        c._kf = {x: base._kf[x].clone() for x in ("k", "v")}
-        c._pk = {x: base._pk[x].clone() for x in ("k", "v")}
-        c._sc = {x: base._sc[x].clone() for x in ("k", "v")}
-        caches.append(c)
+    kt, vt = torch.from_numpy(k).to(dev), torch.from_numpy(v).to(dev)
+    if args.fp16:
+        # replicas so bytes come from HBM
+        kvs = [(kt, vt)] + [(kt.clone(), vt.clone()) for _ in range(args.replicas - 1)]
+    else:
+        base = ChronoQuantCache(stride_k=cfg.stride_k, stride_v=cfg.stride_v,
+                                delta_bits_k=cfg.delta_bits_k, delta_bits_v=cfg.delta_bits_v,
+                                dead_zone_k=cfg.dead_zone_k, dead_zone_v=cfg.dead_zone_v,
+                                capacity=cfg.T)
+        base.update_and_fetch(kt, vt)
+        import copy
+        caches = [base]
+        for _ in range(args.replicas - 1):  # cycle replicas so bytes come from HBM
+            c = copy.copy(base)
+            c._kf = {x: base._kf[x].clone() for x in ("k", "v")}
+            c._pk = {x: base._pk[x].clone() for x in ("k", "v")}
+            c._sc = {x: base._sc[x].clone() for x in ("k", "v")}
+            caches.append(c)
+        descs = [c._descriptor() for c in caches]
     q = torch.from_numpy(synth.make_q(cfg)).to(dev)
     out = torch.empty_like(q)
     L = _lib.load()
     B, nq, H = cfg.B, cfg.n_q_heads, cfg.n_kv_heads
     need = L.cq_decode_workspace_size(B, H, nq, cfg.head_dim, cfg.T)
     ws = torch.zeros(need, dtype=torch.uint8, device=dev)
-    descs = [c._descriptor() for c in caches]
     stream = torch.cuda.current_stream().cuda_stream
     spans, per_phase = [], []
     nsplit_seen = None
     for i in range(args.launches + 5):
         ws[_COUNTER_REGION:].zero_()
         torch.cuda.synchronize()
-        st = L.cq_decode_attn(descs[i % len(descs)], q.data_ptr(), _lib.CQ_F16, nq,
-                              cfg.head_dim ** -0.5, None, cfg.T, cfg.T, out.data_ptr(),
-                              _lib.CQ_F16, ws.data_ptr(), ws.numel(), stream)
+        if args.fp16:
+            kk, vv = kvs[i % len(kvs)]
+            st = L.cq_fp16_decode_attn(kk.data_ptr(), vv.data_ptr(), cfg.T, B, H, cfg.head_dim,
+                                       q.data_ptr(), _lib.CQ_F16, nq, cfg.head_dim ** -0.5, None,
+                                       cfg.T, cfg.T, out.data_ptr(), _lib.CQ_F16, ws.data_ptr(),
+                                       ws.numel(), stream)
+        else:
+            st = L.cq_decode_attn(descs[i % len(descs)], q.data_ptr(), _lib.CQ_F16, nq,
+                                  cfg.head_dim ** -0.5, None, cfg.T, cfg.T, out.data_ptr(),
+                                  _lib.CQ_F16, ws.data_ptr(), ws.numel(), stream)
         assert st == 0, _lib.status_string(st)
         torch.cuda.synchronize()
         if i < 5:
@@ -109,7 +127,8 @@ def main() -> None:
         spans.append(rel[:, 5].max())
         per_phase.append([(np.median(rel[:, p]), rel[:, p].max()) for p in range(6)])
     pp = np.array(per_phase)  # [launch, phase, (median, max)]
-    print(f"config {args.config}: B={B} H={H} nq={nq} T={cfg.T}; {nsplit_seen} splits per kv head, "
+    what = "fp16 decode" if args.fp16 else "config"
+    print(f"{what} {args.config}: B={B} H={H} nq={nq} T={cfg.T}; {nsplit_seen} splits per kv head, "
           f"{nsplit_seen * H * B} workgroups; {args.launches} eager launches over "
           f"{args.replicas} cache replicas")
     print(f"{'phase':<18}{'median wg (us)':>16}{'latest wg (us)':>16}")
