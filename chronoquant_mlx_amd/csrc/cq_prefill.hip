@@ -54,7 +54,6 @@ constexpr int kThreads = 1024;   // 16 waves: 16 rows each
 // c4 chunk against other paddings of the same block (136: 117.6-118.0 us,
 // 144: 114.4-114.6, 152: 117.5-119.1, 160: 116.6-117.2, 168: 115.6-118.9).
 constexpr int kKStride = kD + 16;
-constexpr int kVStride = kKeys + 8;   // V^T block row stride (fp16 elements)
 constexpr float kTau = 8.f;
 
 struct PrefillArgs {
@@ -141,15 +140,23 @@ __device__ __forceinline__ uint4 rebuild8(uint32_t cw, uint4 a, h2_t s2, uint32_
                as_u(a57 + c57 * s2)};
 }
 
-// Column (fp16 index) of 4-key group g in V^T row `row`: groups swapped in
-// pairs on rows 8..15 of every 16.
-__device__ __forceinline__ int vt_col(int row, int g) { return 4 * (g ^ ((row >> 3) & 1)); }
+// LDS transpose read (gfx950 ds_read_b64_tr_b16): within each group of 16
+// lanes, lane 4j + c addresses 4 fp16 (c: a 4-column slice of row j) and
+// lane r of the group receives element r % 4 of lanes r / 4, r / 4 + 4,
+// r / 4 + 8, r / 4 + 12 (checked on the device: rows j = 0..3 of the
+// group's 4 x 16 tile come back as the 4 values of column r).
+typedef short s4_t __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ uint2 lds_read_tr16(const uint16_t *p) {
+  const s4_t v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (__attribute__((address_space(3))) s4_t *)(p));
+  return __builtin_bit_cast(uint2, v);
+}
 
 // Two block buffers: block kb + 1 is rebuilt into one while block kb's
 // products read the other, so each block needs one barrier.
 struct alignas(16) PrefillLds {
   uint16_t k[2][kKeys][kKStride];  // K block, [key][dim (grouped order)]
-  uint16_t v[2][kD][kVStride];     // V block transposed, [dim (grouped order)][key]
+  uint16_t v[2][kKeys][kKStride];  // V block, [key][dim (grouped order)]
 };
 
 // Split epilogue: this workgroup's rows' (m, l, o) go to the workspace with
@@ -325,21 +332,15 @@ void prefill_mfma_kernel(PrefillArgs a) {
 
   // Block staging: waves 0-7 load and rebuild the K block, waves 8-15 the V
   // block, so that each thread holds one component's raw data in registers.
-  //   K (thread st = tid): key (st % 16) + 16 (st / 128), dims 16 ((st / 16)
-  //   % 8) .. +15 (2 code words): the lanes of one 16-byte LDS write phase
-  //   are consecutive keys (rows kKStride / 2 dwords apart).
-  //   V (thread st = tid - 512): code word st / 32 (dims 8w .. 8w+7), keys
-  //   2 (st % 32), +1.  The lanes of a 32-bit LDS write then cover keys
-  //   0..63 of one V^T row, and the two rows of a 64-lane phase are 8 apart
-  //   (8 * 36 dwords = 32 banks): conflict-free.  V^T rows 8..15 of every 16
-  //   hold their 4-key groups swapped in pairs (vt_col), so that the P.V
-  //   reads of rows r and r + 8, which share banks at 32 banks, touch
-  //   different ones.
+  // Both blocks are row-major ([key][dim]); thread st (tid % 512) takes key
+  // (st % 16) + 16 (st / 128), dims 16 ((st / 16) % 8) .. +15 (2 code
+  // words): the lanes of one 16-byte LDS write phase are consecutive keys
+  // (rows kKStride / 2 dwords apart).  The P.V product reads V's operand
+  // columns with transpose reads.
   // the component is wave-uniform: keep it scalar, so that the buffer
   // resources below are too (per-lane resources put every load in a
   // compiler waterfall loop)
   const int c = __builtin_amdgcn_readfirstlane(tid < kThreads / 2 ? 0 : 1);
-  const bool kside = c == 0;
   const int st = tid & (kThreads / 2 - 1);
   const int stride = a.stride[c];
   const float istride = a.inv_stride[c];
@@ -348,11 +349,10 @@ void prefill_mfma_kernel(PrefillArgs a) {
   const __amdgpu_buffer_rsrc_t r_pk = make_rsrc(a.pk[c] + bh * a.cap_pf[c] * 16, (uint32_t)(a.cap_pf[c] * 64));
   const __amdgpu_buffer_rsrc_t r_sc = make_rsrc(a.sc[c] + bh * a.cap_pf[c], (uint32_t)(a.cap_pf[c] * 2));
   const int kkey = (st & 15) | ((st >> 7) << 4), ke = (st >> 4) & 7;
-  const int vw = st >> 5, vkp = st & 31;
   uint32_t magic;  // fp16 1024 in both halves, an opaque VGPR for the byte permutes
   asm volatile("v_mov_b32 %0, 0x64006400" : "=v"(magic));
-  uint32_t r_cw[2], r_s[2];  // K: code words 2ke, 2ke + 1, scale in r_s[0]; V: per key j
-  uint4 r_an[2];             // K: anchor dims 16 ke + 8j ..; V: per key j, dims 8vw ..
+  uint32_t r_cw[2], r_s;  // code words 2ke, 2ke + 1 of key kkey, its scale
+  uint4 r_an[2];          // its anchor row, dims 16 ke + 8j ..
   // token t -> anchor index g (-1 past the end) and P-frame slot (-1:
   // I-frame or past the end)
   auto locate = [&](int t, int &g, int &slot) {
@@ -367,53 +367,24 @@ void prefill_mfma_kernel(PrefillArgs a) {
     if (!in) g = -1;
   };
   auto load_block = [&](int k0) {
-    if (kside) {
-      int g, slot;
-      locate(k0 + kkey, g, slot);
-      const uint32_t arow = g >= 0 ? (uint32_t)g * 256u : 0x80000000u;
-      r_s[0] = bload16(r_sc, (uint32_t)slot * 2u);
-      const uint2 cw = bload64(r_pk, (uint32_t)slot * 64u + 8u * ke);
-      r_cw[0] = cw.x;
-      r_cw[1] = cw.y;
+    int g, slot;
+    locate(k0 + kkey, g, slot);
+    const uint32_t arow = g >= 0 ? (uint32_t)g * 256u : 0x80000000u;
+    r_s = bload16(r_sc, (uint32_t)slot * 2u);
+    const uint2 cw = bload64(r_pk, (uint32_t)slot * 64u + 8u * ke);
+    r_cw[0] = cw.x;
+    r_cw[1] = cw.y;
 #pragma unroll
-      for (int j = 0; j < 2; ++j) r_an[j] = bload128(r_kf, arow + 32u * ke + 16u * j);
-    } else {
-#pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        int g, slot;
-        locate(k0 + 2 * vkp + j, g, slot);
-        const uint32_t arow = g >= 0 ? (uint32_t)g * 256u : 0x80000000u;
-        r_s[j] = bload16(r_sc, (uint32_t)slot * 2u);
-        r_cw[j] = bload32(r_pk, (uint32_t)slot * 64u + 4u * vw);
-        r_an[j] = bload128(r_kf, arow + 16u * vw);
-      }
-    }
+    for (int j = 0; j < 2; ++j) r_an[j] = bload128(r_kf, arow + 32u * ke + 16u * j);
   };
 
   // ---- 1. rebuild the staged block: K (waves 0-7) or V (waves 8-15) into
   // LDS buffer `buf` --------------------------------------------------------------
   auto rebuild = [&](int buf) {
-    if (kside) {
-      const h2_t s2 = as_h2(r_s[0] * 0x10001u);
-      uint4 *dst = (uint4 *)&lds.k[buf][kkey][16 * ke];
+    const h2_t s2 = as_h2(r_s * 0x10001u);
+    uint4 *dst = (uint4 *)&(c == 0 ? lds.k[buf] : lds.v[buf])[kkey][16 * ke];
 #pragma unroll
-      for (int j = 0; j < 2; ++j) dst[j] = rebuild8(r_cw[j], r_an[j], s2, magic);
-    } else {
-      uint4 r[2];
-#pragma unroll
-      for (int j = 0; j < 2; ++j) r[j] = rebuild8(r_cw[j], r_an[j], as_h2(r_s[j] * 0x10001u), magic);
-      // transpose: row 8w + i of V^T holds grouped-order dim i of the 2 keys
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const int dw = i >> 1;
-        const uint32_t sel = (i & 1) ? 0x07060302u : 0x05040100u;
-        const uint32_t w0 = dw == 0 ? r[0].x : dw == 1 ? r[0].y : dw == 2 ? r[0].z : r[0].w;
-        const uint32_t w1 = dw == 0 ? r[1].x : dw == 1 ? r[1].y : dw == 2 ? r[1].z : r[1].w;
-        const int row = 8 * vw + i;
-        *(uint32_t *)&lds.v[buf][row][vt_col(row, vkp >> 1) + 2 * (vkp & 1)] =
-            __builtin_amdgcn_perm(w1, w0, sel);
-      }
-    }
+    for (int j = 0; j < 2; ++j) dst[j] = rebuild8(r_cw[j], r_an[j], s2, magic);
   };
 
   // Pipeline: while block kb's products read one LDS buffer, the waves
@@ -517,15 +488,18 @@ void prefill_mfma_kernel(PrefillArgs a) {
       }
     }
     // ---- 4. O += P . V: K index 8kg + e = key 16(2P) + 4kg + e (e < 4) or
-    // 16(2P+1) + 4kg + e - 4 --------------------------------------------------------
+    // 16(2P+1) + 4kg + e - 4.  B operand of dim tile dt: lane (n, kg) needs
+    // V[those keys][16dt + n]; with the transpose read, lane 4j + c of
+    // group kg addresses keys 32P + 4kg + j (+ 16), dims 16dt + 4c .. +3 --
 #pragma unroll
     for (int P = 0; P < 2; ++P) {
       const h8_t ap = h8_of(as_u(pp[2 * P][0]), as_u(pp[2 * P][1]), as_u(pp[2 * P + 1][0]),
                             as_u(pp[2 * P + 1][1]));
+      const uint16_t *vrow = &lds.v[cur][32 * P + 4 * kg + (col >> 2)][4 * (col & 3)];
 #pragma unroll
       for (int dt = 0; dt < 8; ++dt) {
-        const uint2 v0 = *(const uint2 *)&lds.v[cur][16 * dt + col][vt_col(col, 8 * P + kg)];
-        const uint2 v1 = *(const uint2 *)&lds.v[cur][16 * dt + col][vt_col(col, 8 * P + 4 + kg)];
+        const uint2 v0 = lds_read_tr16(vrow + 16 * dt);
+        const uint2 v1 = lds_read_tr16(vrow + 16 * kKStride + 16 * dt);
         acc[dt] = mfma32(ap, h8_of(v0.x, v0.y, v1.x, v1.y), acc[dt]);
       }
     }
