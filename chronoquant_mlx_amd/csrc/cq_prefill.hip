@@ -366,16 +366,51 @@ void prefill_mfma_kernel(PrefillArgs a) {
     }
     if (!in) g = -1;
   };
-  auto load_block = [&](int k0) {
+  // Staging offsets of key t = k0 + kkey: scale, code words, anchor row
+  // (offsets past a buffer read zeros: slot -1 of an I-frame or past the
+  // end, anchor -1 past the end).
+  auto offsets_of = [&](int t, uint32_t &o_sc, uint32_t &o_cw, uint32_t &o_an) {
     int g, slot;
-    locate(k0 + kkey, g, slot);
-    const uint32_t arow = g >= 0 ? (uint32_t)g * 256u : 0x80000000u;
-    r_s = bload16(r_sc, (uint32_t)slot * 2u);
-    const uint2 cw = bload64(r_pk, (uint32_t)slot * 64u + 8u * ke);
+    locate(t, g, slot);
+    o_an = g >= 0 ? (uint32_t)g * 256u + 32u * ke : 0x80000000u;
+    o_sc = (uint32_t)slot * 2u;
+    o_cw = (uint32_t)slot * 64u + 8u * ke;
+  };
+  // Blocks are staged in increasing order, 64 keys apart.  With a
+  // power-of-two stride <= 64 a key's frame type is the same in every block
+  // and its anchor and slot advance by fixed steps, so the offsets are kept
+  // and stepped (one compare per block for the end of the cache) instead of
+  // recomputed.
+  const bool stepped = Pow2 && lstride <= 6;  // uniform
+  const int g_step = 64 >> lstride;
+  const bool pframe = (kkey & mstride) != 0;
+  uint32_t s_sc = 0, s_cw = 0, s_an = 0;  // the next block's offsets (stepped)
+  int s_t = 0;
+  if (stepped && kb_lo < kb_hi) offsets_of(kb_lo * kKeys + kkey, s_sc, s_cw, s_an);
+  s_t = kb_lo * kKeys + kkey;
+  const uint32_t d_sc = pframe ? 2u * (uint32_t)(64 - g_step) : 0u;
+  const uint32_t d_cw = pframe ? 64u * (uint32_t)(64 - g_step) : 0u;
+  const uint32_t d_an = 256u * (uint32_t)g_step;
+  auto load_block = [&](int k0) {
+    uint32_t o_sc, o_cw, o_an;
+    if (stepped) {
+      const bool in = s_t < T;
+      o_sc = in ? s_sc : 0x80000000u;
+      o_cw = in ? s_cw : 0x80000000u;
+      o_an = in ? s_an : 0x80000000u;
+      s_t += kKeys;
+      s_sc += d_sc;
+      s_cw += d_cw;
+      s_an += d_an;
+    } else {
+      offsets_of(k0 + kkey, o_sc, o_cw, o_an);
+    }
+    r_s = bload16(r_sc, o_sc);
+    const uint2 cw = bload64(r_pk, o_cw);
     r_cw[0] = cw.x;
     r_cw[1] = cw.y;
 #pragma unroll
-    for (int j = 0; j < 2; ++j) r_an[j] = bload128(r_kf, arow + 32u * ke + 16u * j);
+    for (int j = 0; j < 2; ++j) r_an[j] = bload128(r_kf, o_an + 16u * j);
   };
 
   // ---- 1. rebuild the staged block: K (waves 0-7) or V (waves 8-15) into
