@@ -54,6 +54,10 @@ constexpr int kThreads = 1024;   // 16 waves: 16 rows each
 // c4 chunk against other paddings of the same block (136: 117.6-118.0 us,
 // 144: 114.4-114.6, 152: 117.5-119.1, 160: 116.6-117.2, 168: 115.6-118.9).
 constexpr int kKStride = kD + 16;
+// V block row stride (fp16 elements).  Measured on the c4 chunk with the
+// transpose-read P.V: 144: 104.6-105.1 us, 136: 106.4-106.7, 152:
+// 106.4-107.0, 160: 108.6-109.0.
+constexpr int kVStride = kD + 16;
 constexpr float kTau = 8.f;
 
 struct PrefillArgs {
@@ -156,7 +160,7 @@ __device__ __forceinline__ uint2 lds_read_tr16(const uint16_t *p) {
 // products read the other, so each block needs one barrier.
 struct alignas(16) PrefillLds {
   uint16_t k[2][kKeys][kKStride];  // K block, [key][dim (grouped order)]
-  uint16_t v[2][kKeys][kKStride];  // V block, [key][dim (grouped order)]
+  uint16_t v[2][kKeys][kVStride];  // V block, [key][dim (grouped order)]
 };
 
 // Split epilogue: this workgroup's rows' (m, l, o) go to the workspace with
@@ -417,7 +421,7 @@ void prefill_mfma_kernel(PrefillArgs a) {
   // LDS buffer `buf` --------------------------------------------------------------
   auto rebuild = [&](int buf) {
     const h2_t s2 = as_h2(r_s * 0x10001u);
-    uint4 *dst = (uint4 *)&(c == 0 ? lds.k[buf] : lds.v[buf])[kkey][16 * ke];
+    uint4 *dst = (uint4 *)(c == 0 ? &lds.k[buf][kkey][16 * ke] : &lds.v[buf][kkey][16 * ke]);
 #pragma unroll
     for (int j = 0; j < 2; ++j) dst[j] = rebuild8(r_cw[j], r_an[j], s2, magic);
   };
@@ -534,7 +538,7 @@ void prefill_mfma_kernel(PrefillArgs a) {
 #pragma unroll
       for (int dt = 0; dt < 8; ++dt) {
         const uint2 v0 = lds_read_tr16(vrow + 16 * dt);
-        const uint2 v1 = lds_read_tr16(vrow + 16 * kKStride + 16 * dt);
+        const uint2 v1 = lds_read_tr16(vrow + 16 * kVStride + 16 * dt);
         acc[dt] = mfma32(ap, h8_of(v0.x, v0.y, v1.x, v1.y), acc[dt]);
       }
     }
