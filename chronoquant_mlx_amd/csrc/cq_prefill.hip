@@ -27,9 +27,6 @@
 // to the workspace, and the last of a tile's splits to finish (a ticket on a
 // per-(sequence, kv head, tile) counter) merges them by log-sum-exp, as the
 // decode's split combine does.
-// Inside each 8-dim group the LDS blocks and the Q fragment use the dim order
-// {0,2,4,6,1,3,5,7}, the order the nibble unpack produces; the output store
-// undoes it.
 #include <hip/hip_runtime.h>
 #include <math.h>
 
@@ -123,25 +120,24 @@ __device__ __forceinline__ uint32_t bload16(__amdgpu_buffer_rsrc_t r, uint32_t o
 }
 
 // One code word (8 nibbles, dims 0..7 of a group) and the group's fp16
-// anchor (a01, a23, a45, a67) -> the rebuilt fp16 values as pairs
-// (0,2) (4,6) (1,3) (5,7): fp16(a + fp16(fp16(n - 8) * s)).  A nibble becomes
-// fp16 1024 + n by a byte permute against the magic constant; subtracting
+// anchor (a01, a23, a45, a67) -> the rebuilt fp16 values in dim order:
+// fp16(a + fp16(fp16(n - 8) * s)).  The low and high nibbles of the bytes
+// are interleaved into bytes n0 n1 n2 n3 / n4 n5 n6 n7, then a byte permute
+// against the magic constant makes each nibble fp16 1024 + n; subtracting
 // 1032 is exact.  Codes past the end of the cache read as 0 and the scale as
 // 0, so c * s = -0 and an I-frame row is its anchor exactly.
 __device__ __forceinline__ uint4 rebuild8(uint32_t cw, uint4 a, h2_t s2, uint32_t magic) {
   const uint32_t lo = cw & 0x0F0F0F0Fu, hi = (cw >> 4) & 0x0F0F0F0Fu;
+  const uint32_t x0 = __builtin_amdgcn_perm(hi, lo, 0x05010400u);  // bytes n0 n1 n2 n3
+  const uint32_t x1 = __builtin_amdgcn_perm(hi, lo, 0x07030602u);  // bytes n4 n5 n6 n7
   const h2_t bias = {(_Float16)-1032.f, (_Float16)-1032.f};
-  const uint32_t sel_a = 0x07010500u, sel_b = 0x07030502u;  // bytes (0,1) / (2,3) of the nibbles
-  const h2_t c02 = as_h2(__builtin_amdgcn_perm(magic, lo, sel_a)) + bias;
-  const h2_t c46 = as_h2(__builtin_amdgcn_perm(magic, lo, sel_b)) + bias;
-  const h2_t c13 = as_h2(__builtin_amdgcn_perm(magic, hi, sel_a)) + bias;
-  const h2_t c57 = as_h2(__builtin_amdgcn_perm(magic, hi, sel_b)) + bias;
-  const h2_t a02 = as_h2(__builtin_amdgcn_perm(a.y, a.x, 0x05040100u));
-  const h2_t a46 = as_h2(__builtin_amdgcn_perm(a.w, a.z, 0x05040100u));
-  const h2_t a13 = as_h2(__builtin_amdgcn_perm(a.y, a.x, 0x07060302u));
-  const h2_t a57 = as_h2(__builtin_amdgcn_perm(a.w, a.z, 0x07060302u));
-  return uint4{as_u(a02 + c02 * s2), as_u(a46 + c46 * s2), as_u(a13 + c13 * s2),
-               as_u(a57 + c57 * s2)};
+  const uint32_t sel_a = 0x07010500u, sel_b = 0x07030502u;  // bytes (0,1) / (2,3) of x
+  const h2_t c01 = as_h2(__builtin_amdgcn_perm(magic, x0, sel_a)) + bias;
+  const h2_t c23 = as_h2(__builtin_amdgcn_perm(magic, x0, sel_b)) + bias;
+  const h2_t c45 = as_h2(__builtin_amdgcn_perm(magic, x1, sel_a)) + bias;
+  const h2_t c67 = as_h2(__builtin_amdgcn_perm(magic, x1, sel_b)) + bias;
+  return uint4{as_u(as_h2(a.x) + c01 * s2), as_u(as_h2(a.y) + c23 * s2),
+               as_u(as_h2(a.z) + c45 * s2), as_u(as_h2(a.w) + c67 * s2)};
 }
 
 // LDS transpose read (gfx950 ds_read_b64_tr_b16): within each group of 16
@@ -159,16 +155,16 @@ __device__ __forceinline__ uint2 lds_read_tr16(const uint16_t *p) {
 // Two block buffers: block kb + 1 is rebuilt into one while block kb's
 // products read the other, so each block needs one barrier.
 struct alignas(16) PrefillLds {
-  uint16_t k[2][kKeys][kKStride];  // K block, [key][dim (grouped order)]
-  uint16_t v[2][kKeys][kVStride];  // V block, [key][dim (grouped order)]
+  uint16_t k[2][kKeys][kKStride];  // K block, [key][dim]
+  uint16_t v[2][kKeys][kVStride];  // V block, [key][dim]
 };
 
 // Split epilogue: this workgroup's rows' (m, l, o) go to the workspace with
 // device-scope stores; the last of the tile's nsplit workgroups to take a
 // ticket folds every row's partials by log-sum-exp, writes the output and
 // resets the counter.  Row R of the tile is position p0 + R / G, head R % G;
-// lane (col, kg) of wave w holds o of rows 16w + 4kg + r at grouped dims
-// 16dt + col, and m, l of row 16w + col.
+// lane (col, kg) of wave w holds o of rows 16w + 4kg + r at dims 16dt + col,
+// and m, l of row 16w + col.
 template <bool Bf16>
 __device__ __forceinline__ void split_epilogue(const PrefillArgs &a, int b, int h, int tile,
                                                int split, int64_t p0, float m_run, float l_run,
@@ -177,7 +173,6 @@ __device__ __forceinline__ void split_epilogue(const PrefillArgs &a, int b, int 
   const int col = lane & 15, kg = lane >> 4;
   const int G = a.G, ns = a.nsplit;
   const int64_t L = a.n_q;
-  const int perm8[8] = {0, 2, 4, 6, 1, 3, 5, 7};
   const int64_t rows = (int64_t)a.B * a.nq * L;  // global rows (host-bounded below 2^31 / (ns D 4))
   const __amdgpu_buffer_rsrc_t racc = make_rsrc(a.part_acc, (uint32_t)(rows * ns * kD * 4));
   const __amdgpu_buffer_rsrc_t rml = make_rsrc(a.part_ml, (uint32_t)(rows * ns * 8));
@@ -191,8 +186,7 @@ __device__ __forceinline__ void split_epilogue(const PrefillArgs &a, int b, int 
       const uint32_t base = (uint32_t)((grow(R) * ns + split) * kD);
 #pragma unroll
       for (int dt = 0; dt < 8; ++dt) {
-        const int gi = 16 * dt + col;
-        store_dev1(racc, 4u * (base + 8 * (gi >> 3) + perm8[gi & 7]), acc[dt][r]);
+        store_dev1(racc, 4u * (base + 16 * dt + col), acc[dt][r]);
       }
     }
   }
@@ -287,8 +281,8 @@ void prefill_mfma_kernel(PrefillArgs a) {
   const int64_t L = a.n_q;
   const int qbase = T - (int)L;  // position of query 0
 
-  // ---- Q fragment: row (16 wave + col), dims of K-step s in the grouped
-  // order; B operand of S^T = K . Q^T ----------------------------------------
+  // ---- Q fragment: row (16 wave + col), dims 32s + 8kg .. +7 of K-step s;
+  // B operand of S^T = K . Q^T -------------------------------------------------
   const int my_row = 16 * wave + col;
   const int64_t my_pos = p0 + my_row / G;
   const int my_head = my_row % G;
@@ -313,9 +307,7 @@ void prefill_mfma_kernel(PrefillArgs a) {
         v = __builtin_bit_cast(h8_t, u) * sc16;  // fp16(q * fp16(scale))
       }
       if (!my_valid) v = h8_t{};
-      const uint4 w = __builtin_bit_cast(uint4, v);
-      qf[s] = h8_of(__builtin_amdgcn_perm(w.y, w.x, 0x05040100u), __builtin_amdgcn_perm(w.w, w.z, 0x05040100u),
-                    __builtin_amdgcn_perm(w.y, w.x, 0x07060302u), __builtin_amdgcn_perm(w.w, w.z, 0x07060302u));
+      qf[s] = v;
     }
   }
   // causal limit of this lane's row (scores rows = lane col)
@@ -545,9 +537,8 @@ void prefill_mfma_kernel(PrefillArgs a) {
     __syncthreads();  // buffer cur is rebuilt next iteration
   }
 
-  // ---- output: lane (col = grouped dim 16dt + col, kg) holds rows 4kg + r -------
+  // ---- output: lane (col = dim 16dt + col, kg) holds rows 4kg + r ---------------
   l_run = xor32_sum(xor16_sum(l_run));
-  const int perm8[8] = {0, 2, 4, 6, 1, 3, 5, 7};
   if (a.nsplit > 1) {
     split_epilogue<Bf16>(a, b, h, tile, split, p0, m_run, l_run, acc);
     return;
@@ -563,9 +554,7 @@ void prefill_mfma_kernel(PrefillArgs a) {
       uint16_t *orow = a.out + (((int64_t)b * a.nq + h * G + head) * L + pos) * kD;
 #pragma unroll
       for (int dt = 0; dt < 8; ++dt) {
-        const int gi = 16 * dt + col;
-        const int dim = 8 * (gi >> 3) + perm8[gi & 7];
-        orow[dim] = Bf16 ? f32_to_bf16_bits(acc[dt][r] * inv)
+        orow[16 * dt + col] = Bf16 ? f32_to_bf16_bits(acc[dt][r] * inv)
                          : __builtin_bit_cast(uint16_t, (_Float16)(acc[dt][r] * inv));
       }
     }
