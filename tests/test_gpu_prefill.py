@@ -48,7 +48,11 @@ def test_gqa_ratios(G, H):
                                     dict(stride_k=1, stride_v=8),
                                     dict(stride_k=5, stride_v=12),
                                     dict(stride_k=4, stride_v=4, bits_k=3, bits_v=3, dz_k=0.2,
-                                         dz_v=0.2)])
+                                         dz_v=0.2),
+                                    # power-of-two strides above 64 (offsets recomputed per
+                                    # block, not stepped) and at 64 on both components
+                                    dict(stride_k=128, stride_v=256),
+                                    dict(stride_k=64, stride_v=64)])
 def test_codec_settings(params):
     _check(1, 2, 4, 600, 100, params, seed=7)
 
